@@ -1,0 +1,363 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--all] [--no-cpu-baseline]
+
+Prints ONE JSON line. The headline is BASELINE config 3: Llama-3-8B-shaped
+paged decode attention (B=64, H=32, KV=8, D=128, bf16, contexts log-uniform
+in [128, 8192], K/V pages scattered over a pool 1.2x the pages needed).
+A step is one paged_decode_attention call on inputs already resident in HBM.
+
+value        algorithmic bytes of one call / wall time per step (GB/s):
+             every visible K and V row once, q and out once, the page ids and
+             context lengths (nimbus_amd.workloads.decode_bytes)
+roofline     the partition pass (the dominant kernel) alone, timed with HIP
+             events on the launch stream: algorithmic bytes / its mean
+             duration, against 8 TB/s
+cpu_baseline the CPU oracle (restated nimbus/kernels/reference.py:71-96,
+             batched exact form) on this host's cores, same inputs
+prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
+             prefixes of up to 1024): causal FLOPs / mean kernel time, against
+             the 2.5 PFLOP/s dense bf16 MFMA peak
+mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
+             (eager) + the 60 decodes replayed from a hipGraph padded to 64
+
+Between timed calls the K/V pool rotates over enough copies (>= 1.5 GB) that
+the 256 MB Infinity Cache cannot serve one call's pages to the next.
+--all also times every BASELINE config and writes gpurun_out/bench_configs.json.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "paged-decode HBM GB/s & µs/call @Llama-3-8B shape; prefill TFLOP/s"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+ROTATE_BYTES = 1.5e9
+
+
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--all", action="store_true", help="also time every BASELINE config")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=25.0, help="bound on the CPU baseline's timed work")
+    return ap.parse_args(argv)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------- timing helpers
+
+def event_times_us(fn, steps, stream):
+    """Runs fn(i) for i < steps with a HIP event pair around each call on
+    `stream`; returns the per-call durations in microseconds."""
+    import torch
+
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        evs[i][0].record(stream)
+        fn(i)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e3 for a, b in evs]
+
+
+def rotated_pools(batch, min_bytes=ROTATE_BYTES):
+    """Copies of (q, k_cache, v_cache) so that consecutive calls read
+    distinct memory; the first copy is the batch's own."""
+    pool_bytes = 2 * batch.k_cache.numel() * batch.k_cache.element_size()
+    n = max(2, math.ceil(min_bytes / pool_bytes))
+    pools = [(batch.q, batch.k_cache, batch.v_cache)]
+    for _ in range(n - 1):
+        pools.append((batch.q.clone(), batch.k_cache.clone(), batch.v_cache.clone()))
+    return pools
+
+
+# ---------------------------------------------------------------- decode
+
+def time_decode(batch, steps, warmup, wall=True):
+    import torch
+
+    from nimbus_amd import workloads
+    from nimbus_amd.kernels.paged_attention import decode_workspace_bytes, paged_decode_attention
+
+    p = batch.num_prefills
+    t0 = batch.num_prefill_tokens
+    ctx_lens = batch.decode_context_host()
+    ctx = batch.context_lens[p:]
+    bt = batch.block_tables[p:]
+    maxc = max(ctx_lens)
+    b = len(ctx_lens)
+    h, d = batch.q.shape[1], batch.q.shape[2]
+    kv = batch.k_cache.shape[2]
+    pools = rotated_pools(batch)
+    out = torch.empty_like(batch.q[t0:])
+    ws = torch.empty(max(1, decode_workspace_bytes(b, h, d, maxc)), dtype=torch.uint8, device=batch.q.device)
+    stream = torch.cuda.current_stream()
+
+    def call(i, entry="nimbus_paged_decode"):
+        q, kc, vc = pools[i % len(pools)]
+        paged_decode_attention(q[t0:], kc, vc, ctx, bt, maxc, batch.scale, out=out, workspace=ws, _entry=entry)
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    res = {}
+    if wall:
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        for i in range(steps):
+            call(i)
+        torch.cuda.synchronize()
+        res["ms_per_step"] = (time.perf_counter() - w0) * 1e3 / steps
+    res["call_us"] = statistics.mean(event_times_us(call, steps, stream))
+    res["partition_us"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_partitions"),
+                                                         steps, stream))
+    res["merge_us"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_merge"), steps, stream))
+    res["bytes"] = workloads.decode_bytes(ctx_lens, h, kv, d, batch.q.element_size())
+    res["pools"] = len(pools)
+    res["batch"] = b
+    res["sum_ctx"] = sum(ctx_lens)
+    return res
+
+
+def cpu_decode_baseline(batch, seconds):
+    """The CPU oracle (batched exact form of nimbus/kernels/reference.py:71-96)
+    on CPU copies of the same inputs: one warm-up, then up to 3 timed reps
+    within `seconds`."""
+    import torch
+
+    from nimbus_amd import workloads
+    from oracle import reference
+
+    p = batch.num_prefills
+    t0 = batch.num_prefill_tokens
+    ctx_lens = batch.decode_context_host()
+    q = batch.q[t0:].cpu()
+    kc, vc = batch.k_cache.cpu(), batch.v_cache.cpu()
+    ctx = batch.context_lens[p:].cpu()
+    bt = batch.block_tables[p:].cpu()
+    maxc = max(ctx_lens)
+    h, d, kv = q.shape[1], q.shape[2], kc.shape[2]
+    t = time.perf_counter()
+    reference.paged_decode_attention(q, kc, vc, ctx, bt, maxc, batch.scale)
+    first = time.perf_counter() - t
+    times = []
+    budget = time.perf_counter() + seconds
+    while len(times) < 3 and time.perf_counter() + first < budget:
+        t = time.perf_counter()
+        reference.paged_decode_attention(q, kc, vc, ctx, bt, maxc, batch.scale)
+        times.append(time.perf_counter() - t)
+    if not times:
+        times = [first]
+    med = statistics.median(times)
+    nbytes = workloads.decode_bytes(ctx_lens, h, kv, d, q.element_size())
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": nbytes / med / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"full llama3_decode batch (B={len(ctx_lens)}, sum ctx {sum(ctx_lens)}) through the batched "
+                   f"CPU oracle, median of {len(times)} reps after 1 warm-up: {med * 1e3:.1f} ms/call; "
+                   f"host {cpu_model}, os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+# ---------------------------------------------------------------- prefill and the mixed step
+
+def time_prefill(batch, steps, warmup):
+    import torch
+
+    from nimbus_amd import workloads
+    from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
+
+    args = batch.prefill_args()
+    progs = build_programs(args[7], batch.q.device)
+    out = torch.empty_like(args[0])
+
+    def call(i):
+        paged_prefill_attention(*args, progs, out=out)
+
+    for i in range(warmup):
+        call(i)
+    us = statistics.mean(event_times_us(call, steps, torch.cuda.current_stream()))
+    seqs = batch.seqs[:batch.num_prefills]
+    h, d = batch.q.shape[1], batch.q.shape[2]
+    flops = workloads.prefill_flops(seqs, h, d)
+    return {"us_per_call": us, "flops": flops, "tflops": flops / us / 1e6, "tiles": int(progs[0].numel())}
+
+
+def time_mixed_step(batch, steps, warmup):
+    """write_kv for every token + prefill (eager) + decode via hipGraph at padded 64."""
+    import torch
+
+    from nimbus_amd.graphs import DecodeAttentionGraphs
+    from nimbus_amd.kernels.cache_ops import write_kv
+    from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
+
+    nb = batch.k_cache.shape[0]
+    kc = torch.cat([batch.k_cache, torch.zeros_like(batch.k_cache[:1])])  # + scratch block
+    vc = torch.cat([batch.v_cache, torch.zeros_like(batch.v_cache[:1])])
+    graphs = DecodeAttentionGraphs(kc, vc, num_heads=batch.q.shape[1], scale=batch.scale, max_model_len=8192,
+                                   max_batch=64, scratch_block=nb)
+    graphs.capture()
+    pa = batch.prefill_args()
+    progs = build_programs(pa[7], batch.q.device)
+    p_tok = batch.num_prefill_tokens
+    da = batch.decode_args()
+    out = torch.empty_like(batch.q)
+    # The decode graph does its own slot write for its tokens; the eager write covers the prefill tokens.
+    gb = graphs.load(da[0], batch.k[p_tok:], batch.v[p_tok:], batch.slot_mapping[p_tok:], da[3], da[4])
+
+    def step(i):
+        write_kv(batch.k[:p_tok], batch.v[:p_tok], kc, vc, batch.slot_mapping[:p_tok])
+        paged_prefill_attention(pa[0], kc, vc, pa[3], pa[4], pa[5], pa[6], pa[7], pa[8], progs, out=out[:p_tok])
+        graphs.replay(gb)
+
+    for i in range(warmup):
+        step(i)
+    us = event_times_us(step, steps, torch.cuda.current_stream())
+    replay_us = event_times_us(lambda i: graphs.replay(gb), steps, torch.cuda.current_stream())
+    return {"step_us": statistics.mean(us), "decode_graph_replay_us": statistics.mean(replay_us),
+            "padded_batch": gb, "tokens": int(batch.q.shape[0])}
+
+
+# ---------------------------------------------------------------- --all
+
+def all_configs(steps, warmup):
+    import torch
+
+    from nimbus_amd import workloads
+
+    rows = {}
+    for name in ("tinyllama_decode", "llama3_decode", "llama3_long_decode"):
+        log(f"config {name}")
+        b = workloads.CONFIGS[name]("cuda")
+        r = time_decode(b, steps, warmup, wall=False)
+        r["GBps_call"] = r["bytes"] / r["call_us"] / 1e3
+        r["GBps_partition_pass"] = r["bytes"] / r["partition_us"] / 1e3
+        r["frac_hbm_peak_partition_pass"] = r["GBps_partition_pass"] / HBM_PEAK_GBS
+        rows[name] = r
+        del b
+        torch.cuda.empty_cache()
+    for name in ("tinyllama_prefill", "llama3_mixed"):
+        log(f"config {name}")
+        b = workloads.CONFIGS[name]("cuda")
+        r = time_prefill(b, steps, warmup)
+        r["frac_mfma_peak"] = r["tflops"] / MFMA_BF16_PEAK_TFLOPS
+        if name == "llama3_mixed":
+            r["mixed_step"] = time_mixed_step(b, steps, warmup)
+        rows[name] = r
+        del b
+        torch.cuda.empty_cache()
+    os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
+    with open(os.path.join(ROOT, "gpurun_out", "bench_configs.json"), "w") as f:
+        json.dump(rows, f, indent=1)
+    for k, v in rows.items():
+        log(f"{k}: " + ", ".join(f"{a}={b:.4g}" if isinstance(b, float) else f"{a}={b}" for a, b in v.items()
+                                 if not isinstance(b, dict)))
+    return rows
+
+
+# ---------------------------------------------------------------- main
+
+def main(argv=None):
+    args = parse(argv)
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); this build has no multi-GPU path: "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from nimbus_amd import _lib, workloads
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    _lib.load()
+    torch.manual_seed(0)
+
+    log("building llama3_decode (config 3)")
+    batch = workloads.llama3_decode("cuda")
+    dec = time_decode(batch, args.steps, args.warmup)
+    log(f"decode: {dec}")
+    part_gbs = dec["bytes"] / dec["partition_us"] / 1e3
+    result = {
+        "metric": METRIC,
+        "value": dec["bytes"] / (dec["ms_per_step"] * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dec["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q, 0.5*N(0,1) K/V, shuffled page tables)",
+        "config": {
+            "workload": "llama3_decode: BASELINE config 3, Llama-3-8B-shaped paged decode attention",
+            "batch": dec["batch"], "heads": 32, "kv_heads": 8, "head_dim": 128, "block_size": 16,
+            "context": "log-uniform [128, 8192], seed 0", "sum_ctx": dec["sum_ctx"],
+            "bytes_per_call": dec["bytes"], "pool_rotation": dec["pools"], "parallelism": "none (1 GPU)",
+        },
+        "us_per_call": dec["call_us"],
+        "roofline": {
+            "kernel": "paged_decode_kernel (partition pass)",
+            "bound": "hbm",
+            "achieved": part_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": part_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "kernel_us": dec["partition_us"],
+            "merge_pass_us": dec["merge_us"],
+        },
+    }
+    if not args.no_prefill:
+        log("building llama3_mixed (config 4)")
+        mixed = workloads.llama3_mixed("cuda")
+        pre = time_prefill(mixed, args.steps, args.warmup)
+        pre["frac_mfma_peak"] = pre["tflops"] / MFMA_BF16_PEAK_TFLOPS
+        result["prefill"] = {"workload": "llama3_mixed prefill part (4 x 512 new on prefix U[0,1024])", **pre,
+                             "peak_tflops": MFMA_BF16_PEAK_TFLOPS}
+        result["mixed_step"] = time_mixed_step(mixed, args.steps, args.warmup)
+        log(f"prefill: {result['prefill']}  mixed: {result['mixed_step']}")
+        del mixed
+    if args.all:
+        result["configs"] = {k: {a: b for a, b in v.items() if not isinstance(b, dict)}
+                             for k, v in all_configs(args.steps, args.warmup).items()}
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle on host cores)")
+        result["cpu_baseline"] = cpu_decode_baseline(batch, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,150 @@
+/*
+ * nimbus_attn.h - C ABI of the MI355X (gfx950) paged-attention library.
+ *
+ * libnimbus_attn.so replaces the GPU side of Nimbus's attention hot path:
+ * the KV slot write, paged decode attention and causal varlen paged prefill
+ * attention. Every entry point takes plain device pointers, element strides
+ * (not bytes), sizes, a dtype code and an opaque hipStream_t; none allocates,
+ * frees, synchronises or reads device memory on the host, so each call can be
+ * recorded into a hipGraph. PyTorch (or any caller) owns every buffer.
+ *
+ * Return value: 0 on success, a negative NIMBUS_ERR_* for arguments rejected
+ * before launch, or a positive hipError_t from the launch itself.
+ *
+ * Caches are [num_blocks, block_size, num_kv_heads, head_dim] with unit
+ * stride in the last dimension (nimbus/cache/kv_cache.py:18-25);
+ * block_size must be 16 and head_dim 64 or 128. Context lengths and block
+ * tables are int32, slot mappings int64 (nimbus/runner.py:77-85).
+ */
+#ifndef NIMBUS_ATTN_H
+#define NIMBUS_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NIMBUS_ATTN_ABI_VERSION 1
+
+/* dtype codes */
+#define NIMBUS_FLOAT16 0
+#define NIMBUS_BFLOAT16 1
+
+/* error codes (negative: rejected before launch) */
+#define NIMBUS_OK 0
+#define NIMBUS_ERR_INVALID (-1)     /* inconsistent sizes or null pointers */
+#define NIMBUS_ERR_UNSUPPORTED (-2) /* shape/dtype outside what the kernels cover */
+#define NIMBUS_ERR_ALIGNMENT (-3)   /* a base or stride breaks 16-byte vector access */
+#define NIMBUS_ERR_WORKSPACE (-4)   /* decode workspace missing or too small */
+
+/* Version of this ABI (NIMBUS_ATTN_ABI_VERSION). */
+int nimbus_attn_abi_version(void);
+
+/* Static text for a return code of any entry point. */
+const char* nimbus_attn_error_string(int code);
+
+/*
+ * KV slot write. Replaces nimbus/kernels/reference.py:14-23 (write_kv:
+ * k_cache.view(-1, KV, D).index_copy_(0, slot_mapping, k), same for v),
+ * called on every backend at nimbus/model/attention.py:78.
+ *
+ * For t < num_tokens: flat slot s = slot_mapping[t] (= block*block_size +
+ * offset, nimbus/runner.py:61) receives k[t] in k_cache and v[t] in v_cache,
+ * bit for bit. k/v rows: element (t, h, d) at t*stride_token + h*stride_head
+ * + d. Caches must be contiguous (the reference views them flat).
+ * Slots outside [0, num_slots) are skipped instead of written. Duplicate
+ * slots leave one of the writers' rows (which one is unspecified, as with
+ * index_copy_).
+ */
+int nimbus_write_kv(const void* k, const void* v, void* k_cache, void* v_cache, const int64_t* slot_mapping,
+                    int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim, int64_t k_stride_token,
+                    int64_t k_stride_head, int64_t v_stride_token, int64_t v_stride_head, int64_t num_slots,
+                    int32_t dtype, void* stream);
+
+/*
+ * Bytes of fp32 workspace nimbus_paged_decode needs for split-context
+ * partial results at this batch, head count, head dim and max_context
+ * (0 when one partition covers max_context). Pure function of its arguments.
+ * Partition size: NIMBUS_DECODE_PARTITION tokens.
+ */
+#define NIMBUS_DECODE_PARTITION 512
+int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
+                                            int64_t max_context);
+
+/*
+ * Paged decode attention. Replaces nimbus/kernels/paged_attention.py:101-146
+ * (paged_decode_attention with _paged_decode_kernel :25-80 and
+ * _merge_partitions_kernel :83-98).
+ *
+ * out[b, h, :] = softmax(scale * q[b, h] . K_b^T) V_b over the first
+ * context_lens[b] tokens of sequence b, read through block_tables[b] from
+ * kv head h / (num_heads / num_kv_heads). q/out: element (b, h, d) at
+ * b*stride_b + h*stride_h + d. The launch grid depends only on batch,
+ * num_kv_heads and max_context (which must be >= every context length);
+ * rows with shorter contexts exit early, so a fixed max_context gives a
+ * graph-capturable call. Page ids outside [0, num_blocks) read page 0
+ * instead of faulting.
+ */
+int nimbus_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                        const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                        int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                        int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
+                        int64_t out_stride_b, int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                        int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t block_size, int64_t max_context, float scale, int32_t dtype, void* stream);
+
+/*
+ * The two passes of nimbus_paged_decode, launchable on their own (same
+ * arguments). nimbus_paged_decode_partitions replaces _paged_decode_kernel
+ * (paged_attention.py:25-80): it writes the final output of every sequence
+ * that fits in one partition and fp32 partials for the others.
+ * nimbus_paged_decode_merge replaces _merge_partitions_kernel
+ * (paged_attention.py:83-98): it combines those partials into the output
+ * (nothing to do, and no launch, when max_context fits in one partition).
+ * Running partitions then merge on one stream equals nimbus_paged_decode.
+ */
+int nimbus_paged_decode_partitions(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                                   const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                                   int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                                   int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
+                                   int64_t out_stride_b, int64_t out_stride_h, void* workspace,
+                                   int64_t workspace_bytes, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t block_size, int64_t max_context, float scale,
+                                   int32_t dtype, void* stream);
+int nimbus_paged_decode_merge(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                              const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                              int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                              int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
+                              int64_t out_stride_b, int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                              int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t block_size, int64_t max_context, float scale, int32_t dtype, void* stream);
+
+/*
+ * Causal varlen paged prefill attention. Replaces
+ * nimbus/kernels/prefill_attention.py:93-119 (paged_prefill_attention and
+ * _paged_prefill_kernel :25-78).
+ *
+ * Sequence i owns query rows [query_start[i], query_start[i+1]) of q; with
+ * q_len = that count and ctx = context_lens[i], its query j sits at absolute
+ * position ctx - q_len + j and attends to cached tokens 0..ctx - q_len + j
+ * (already written by nimbus_write_kv) through block_tables[i].
+ * prog_seq/prog_m is the tile table of build_programs
+ * (prefill_attention.py:81-90): one entry (sequence, first query offset) per
+ * NIMBUS_PREFILL_TILE query positions; num_programs entries.
+ */
+#define NIMBUS_PREFILL_TILE 64
+int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                         const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                         int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                         int64_t bt_stride, int32_t bt_width, const int32_t* query_start,
+                         const int32_t* context_lens, const int32_t* prog_seq, const int32_t* prog_m,
+                         int32_t num_programs, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                         int32_t dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NIMBUS_ATTN_H */

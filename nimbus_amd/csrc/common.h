@@ -1,0 +1,120 @@
+// Shared device helpers for the paged-attention kernels (gfx950 / CDNA4).
+//
+// Element types are carried as raw 16-bit storage (uint16_t) and converted
+// explicitly, so one kernel template serves fp16 and bf16. Matrix products
+// use the CDNA4 MFMA builtins with fp32 accumulation:
+//   16x16x32 (A: 8 elements per lane, k-group = lane / 16)
+//   16x16x16 (A: 4 elements per lane, k-group = lane / 16)
+// Output (C/D) layout of both 16x16 shapes: lane l holds column l % 16 and
+// rows 4 * (l / 16) + r for r = 0..3 (one fp32 per VGPR).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nimbus {
+
+enum DType : int { kFloat16 = 0, kBFloat16 = 1 };
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- conversions
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t x) {
+  return __uint_as_float(static_cast<uint32_t>(x) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t x) {
+  _Float16 h;
+  __builtin_memcpy(&h, &x, 2);
+  return static_cast<float>(h);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  uint16_t x;
+  __builtin_memcpy(&x, &h, 2);
+  return x;
+}
+
+template <int DT> struct Elem;
+
+template <> struct Elem<kFloat16> {
+  __device__ static __forceinline__ float to_f32(uint16_t x) { return f16_to_f32(x); }
+  __device__ static __forceinline__ uint16_t from_f32(float f) { return f32_to_f16(f); }
+};
+
+template <> struct Elem<kBFloat16> {
+  __device__ static __forceinline__ float to_f32(uint16_t x) { return bf16_to_f32(x); }
+  __device__ static __forceinline__ uint16_t from_f32(float f) { return f32_to_bf16(f); }
+};
+
+// ---------------------------------------------------------------- MFMA
+
+// 16x16x32: a, b carry 8 16-bit elements each (4 dwords).
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_16x16x32(u32x4 a, u32x4 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma_16x16x32<kFloat16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                0, 0);
+}
+
+template <>
+__device__ __forceinline__ f32x4 mfma_16x16x32<kBFloat16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+
+// 16x16x16: a, b carry 4 16-bit elements each (2 dwords).
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_16x16x16(u32x2 a, u32x2 b, f32x4 c);
+
+template <>
+__device__ __forceinline__ f32x4 mfma_16x16x16<kFloat16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                               0);
+}
+
+template <>
+__device__ __forceinline__ f32x4 mfma_16x16x16<kBFloat16>(u32x2 a, u32x2 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a), __builtin_bit_cast(s16x4, b), c,
+                                                   0, 0, 0);
+}
+
+// ---------------------------------------------------------------- wave reductions
+
+// Butterfly over the four 16-lane groups of a wave64 (lanes l, l^16, l^32, l^48).
+__device__ __forceinline__ float max_across_groups(float x) {
+  x = fmaxf(x, __shfl_xor(x, 16, 64));
+  x = fmaxf(x, __shfl_xor(x, 32, 64));
+  return x;
+}
+
+__device__ __forceinline__ float sum_across_groups(float x) {
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+
+}  // namespace nimbus

@@ -1,0 +1,55 @@
+"""KV slot write on the GPU.
+
+Drop-in for nimbus/kernels/reference.py:14-23 (`write_kv`), which Nimbus calls
+on every backend before attention (nimbus/model/attention.py:78).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from nimbus_amd import _lib
+
+
+def write_kv(
+    k: torch.Tensor,  # [T, KV, D]
+    v: torch.Tensor,
+    k_cache: torch.Tensor,  # [num_blocks, block_size, KV, D]
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,  # [T] int64
+) -> None:
+    """k_cache.view(-1, KV, D)[slot_mapping[t]] = k[t] (and v), bit for bit.
+
+    Same contract as the reference's two index_copy_ calls: the caches must be
+    viewable flat (contiguous); k and v may be strided in their first two
+    dims (a slice of a fused qkv projection). Slots outside the cache are
+    skipped rather than written.
+    """
+    if k.shape != v.shape or k.dim() != 3:
+        raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must both be [T, KV, D]")
+    if k_cache.shape != v_cache.shape or k_cache.dim() != 4:
+        raise ValueError("k_cache and v_cache must both be [num_blocks, block_size, KV, D]")
+    t, kv, d = k.shape
+    if (kv, d) != tuple(k_cache.shape[2:]):
+        raise ValueError(f"k rows {(kv, d)} do not match the cache's {tuple(k_cache.shape[2:])}")
+    if slot_mapping.shape != (t,) or slot_mapping.dtype != torch.int64:
+        raise ValueError("slot_mapping must be int64 [T]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous (they are written through a flat slot view)")
+    if not (k.dtype == v.dtype == k_cache.dtype == v_cache.dtype):
+        raise ValueError("k, v and the caches must share one dtype")
+    if not (k.is_cuda and k_cache.is_cuda and slot_mapping.is_cuda):
+        raise ValueError("write_kv runs on the GPU only")
+    if t == 0:
+        return
+    if k.stride(-1) != 1:
+        k = k.contiguous()
+    if v.stride(-1) != 1:
+        v = v.contiguous()
+    slot_mapping = slot_mapping.contiguous()
+    lib = _lib.load()
+    rc = lib.nimbus_write_kv(
+        k.data_ptr(), v.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(),
+        t, kv, d, k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        k_cache.shape[0] * k_cache.shape[1], _lib.dtype_code(k.dtype), _lib.stream_of(k))
+    _lib.check(rc, "nimbus_write_kv")

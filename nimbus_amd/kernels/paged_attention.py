@@ -1,0 +1,109 @@
+"""Paged decode attention (one query token per sequence) on the GPU.
+
+Drop-in for nimbus/kernels/paged_attention.py:101-146: same signature, same
+result (within fp16/bf16 rounding of the reference attention), computed by
+paged_decode_kernel + paged_decode_merge_kernel in csrc/paged_decode.hip.
+
+Context is split into PARTITION-token partitions for every sequence, so long
+contexts spread over many workgroups whatever the batch size. The launch grid
+is a function of (batch, KV heads, max_context) only; inside a captured graph
+the caller fixes max_context (Nimbus's DecodeGraphs passes max_model_len,
+cuda_graph.py:52-63) and the same graph serves any context lengths up to it.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from nimbus_amd import _lib
+
+PARTITION = 512  # tokens per split-context partition (NIMBUS_DECODE_PARTITION)
+
+
+def decode_workspace_bytes(batch: int, heads: int, head_dim: int, max_context: int) -> int:
+    return int(_lib.load().nimbus_paged_decode_workspace_bytes(batch, heads, head_dim, max_context))
+
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must both be [num_blocks, block_size, KV, D]")
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("v_cache must share k_cache's strides")
+    if k_cache.stride(-1) != 1:
+        raise ValueError("caches need unit stride in the head dim")
+    if k_cache.dtype != v_cache.dtype:
+        raise ValueError("k_cache and v_cache must share one dtype")
+    if not (k_cache.is_cuda and v_cache.is_cuda):
+        raise ValueError("the paged-attention kernels run on the GPU only")
+
+
+def paged_decode_attention(
+    q: torch.Tensor,  # [B, H, D]
+    k_cache: torch.Tensor,  # [num_blocks, block_size, KV, D]
+    v_cache: torch.Tensor,
+    context_lens: torch.Tensor,  # [B] int32
+    block_tables: torch.Tensor,  # [B, max_blocks] int32
+    max_context: int,
+    scale: float,
+    num_partitions: int | None = None,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    _entry: str = "nimbus_paged_decode",
+) -> torch.Tensor:
+    """out[b, h] = softmax(scale * q[b, h] . K^T) V over sequence b's first
+    context_lens[b] cached tokens (kv head h // (H // KV)).
+
+    max_context must be >= every context length (the reference relies on the
+    same bound for its grid and gather width). num_partitions is accepted for
+    signature compatibility with the Triton wrapper, whose graph capture uses
+    it to pin the grid; here the grid is already pinned by max_context, and
+    the split is always PARTITION tokens, so the value is not used.
+    `out` (optional, not in the reference signature) receives the result in
+    place, e.g. a slice of the backend's flat output. `workspace` (optional)
+    is a caller-owned uint8 buffer of at least decode_workspace_bytes() for the
+    split-context partials; by default one is taken from torch's allocator per
+    call. `_entry` selects one
+    pass of the C ABI (nimbus_paged_decode_partitions / _merge) for timing
+    the passes separately; the default runs both.
+    """
+    del num_partitions
+    if q.dim() != 3:
+        raise ValueError(f"q must be [B, H, D], got {tuple(q.shape)}")
+    b, h, d = q.shape
+    _check_cache(k_cache, v_cache)
+    kv = k_cache.shape[2]
+    if k_cache.shape[3] != d or h % kv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not fit caches {tuple(k_cache.shape)}")
+    if q.dtype != k_cache.dtype:
+        raise ValueError("q and the caches must share one dtype")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype with unit last stride")
+    if b == 0:
+        return out
+    if context_lens.dtype != torch.int32 or block_tables.dtype != torch.int32:
+        raise ValueError("context_lens and block_tables must be int32")
+    if context_lens.shape != (b,) or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise ValueError("context_lens must be [B] and block_tables [B, max_blocks]")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    context_lens = context_lens.contiguous()
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    lib = _lib.load()
+    need = lib.nimbus_paged_decode_workspace_bytes(b, h, d, int(max_context))
+    if workspace is not None:
+        if workspace.numel() * workspace.element_size() < need or not workspace.is_cuda:
+            raise ValueError(f"workspace smaller than the {need} bytes this call needs")
+        ws = workspace
+    else:
+        ws = torch.empty(max(need, 0), dtype=torch.uint8, device=q.device) if need > 0 else None
+    rc = getattr(lib, _entry)(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(), block_tables.stride(0),
+        block_tables.shape[1], context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+        _lib.ptr(ws), 0 if ws is None else ws.numel() * ws.element_size(), b, h, kv, d, k_cache.shape[1], int(max_context), float(scale),
+        _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, _entry)
+    return out

@@ -1,0 +1,98 @@
+"""Causal varlen paged prefill attention on the GPU.
+
+Drop-in for nimbus/kernels/prefill_attention.py:81-119 (`build_programs` and
+`paged_prefill_attention`), computed by paged_prefill_kernel in
+csrc/paged_prefill.hip. A sequence's queries are its newest q_len tokens;
+query j sits at absolute position ctx - q_len + j. This covers fresh prompts
+(q_len == ctx), chunked prefill over a cached prefix and speculative
+verification of several draft tokens.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from nimbus_amd import _lib
+from nimbus_amd.kernels.paged_attention import _check_cache
+
+BLOCK_M = 64  # query positions per tile-table entry (NIMBUS_PREFILL_TILE)
+
+
+def build_programs(query_start_host: list[int], device) -> tuple[torch.Tensor, torch.Tensor]:
+    """(sequence index, first query offset) for every BLOCK_M query tile.
+
+    Same table as nimbus/kernels/prefill_attention.py:81-90, built with NumPy
+    instead of a Python loop and moved to the device in one copy. Nimbus's
+    backend builds it once per step and reuses it in every layer
+    (model/attention.py:82-83).
+    """
+    qs = np.asarray(query_start_host, dtype=np.int64)
+    lens = np.diff(qs) if qs.size > 1 else np.zeros(0, dtype=np.int64)
+    tiles = (lens + BLOCK_M - 1) // BLOCK_M
+    seqs = np.repeat(np.arange(lens.size, dtype=np.int32), tiles)
+    first = np.repeat(np.cumsum(tiles) - tiles, tiles)
+    starts = ((np.arange(seqs.size) - first) * BLOCK_M).astype(np.int32)
+    t = torch.from_numpy(np.stack([seqs, starts]).astype(np.int32)).to(device, non_blocking=True)
+    return t[0], t[1]
+
+
+def paged_prefill_attention(
+    q: torch.Tensor,  # [Tp, H, D]
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    query_start: torch.Tensor,  # [P+1] int32
+    context_lens: torch.Tensor,  # [P] int32
+    block_tables: torch.Tensor,  # [P, max_blocks] int32
+    scale: float,
+    query_start_host: list[int],
+    context_lens_host: list[int],
+    programs: tuple[torch.Tensor, torch.Tensor] | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Causal attention of each sequence's newest tokens over its paged cache.
+
+    The cache must already hold the new tokens' K/V (write_kv runs first, as
+    in nimbus/model/attention.py:78). `programs` is build_programs' tile table
+    (built here when None). `out` (optional, not in the reference signature)
+    receives the result in place.
+    """
+    del context_lens_host  # the kernel reads context_lens on the device
+    if q.dim() != 3:
+        raise ValueError(f"q must be [Tp, H, D], got {tuple(q.shape)}")
+    t, h, d = q.shape
+    _check_cache(k_cache, v_cache)
+    kv = k_cache.shape[2]
+    if k_cache.shape[3] != d or h % kv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not fit caches {tuple(k_cache.shape)}")
+    if q.dtype != k_cache.dtype:
+        raise ValueError("q and the caches must share one dtype")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype with unit last stride")
+    if t == 0 or len(query_start_host) < 2:
+        return out
+    for x, name in ((query_start, "query_start"), (context_lens, "context_lens"), (block_tables, "block_tables")):
+        if x.dtype != torch.int32:
+            raise ValueError(f"{name} must be int32")
+    if block_tables.dim() != 2 or block_tables.shape[0] != len(query_start_host) - 1:
+        raise ValueError("block_tables must be [P, max_blocks]")
+    prog_seq, prog_m = programs if programs is not None else build_programs(query_start_host, q.device)
+    if prog_seq.numel() == 0:
+        return out
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    query_start = query_start.contiguous()
+    context_lens = context_lens.contiguous()
+    lib = _lib.load()
+    rc = lib.nimbus_paged_prefill(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(), block_tables.stride(0),
+        block_tables.shape[1], query_start.data_ptr(), context_lens.data_ptr(), prog_seq.data_ptr(),
+        prog_m.data_ptr(), prog_seq.numel(), out.data_ptr(), out.stride(0), out.stride(1), h, kv, d,
+        k_cache.shape[1], float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, "nimbus_paged_prefill")
+    return out

@@ -1,0 +1,102 @@
+"""CPU: the C-ABI library loads, exports everything include/nimbus_attn.h
+declares, and rejects bad arguments before any launch (no GPU needed)."""
+
+from __future__ import annotations
+
+import os
+import re
+import subprocess
+
+import pytest
+
+from nimbus_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nimbus_attn.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER).read()
+    return re.findall(r"^(?:int|int64_t|const char\*)\s+(nimbus_\w+)\(", text, flags=re.M)
+
+
+def test_header_declares_the_four_launch_paths():
+    names = declared_functions()
+    for want in ("nimbus_write_kv", "nimbus_paged_decode", "nimbus_paged_decode_workspace_bytes",
+                 "nimbus_paged_prefill", "nimbus_attn_abi_version", "nimbus_attn_error_string"):
+        assert want in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    nm = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT (nimbus_\w+)", nm.stdout))
+    for name in declared_functions():
+        assert name in exported, name
+        assert hasattr(lib, name)
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_abi_version_and_error_strings():
+    lib = _lib.load()
+    assert lib.nimbus_attn_abi_version() == _lib.ABI_VERSION
+    for code in (0, -1, -2, -3, -4):
+        assert lib.nimbus_attn_error_string(code)
+    assert b"unknown" in lib.nimbus_attn_error_string(-99)
+
+
+def test_one_hip_runtime_in_process():
+    import torch  # noqa: F401
+
+    _lib.load()
+    assert len(_lib.hip_runtimes()) == 1, _lib.hip_runtimes()
+
+
+def test_workspace_bytes_is_a_pure_size_formula():
+    lib = _lib.load()
+    f = lib.nimbus_paged_decode_workspace_bytes
+    assert f(64, 32, 128, 512) == 0  # one partition: no partials
+    assert f(64, 32, 128, 513) == 64 * 32 * 2 * (128 + 2) * 4
+    assert f(64, 32, 128, 8192) == 64 * 32 * 16 * (128 + 2) * 4
+    assert f(-1, 32, 128, 8192) == -1
+
+
+DUMMY = 1 << 20  # a 16-byte aligned fake address: these calls must return before touching it
+
+
+def _decode(**kw):
+    a = dict(q=DUMMY, qsb=32 * 128, qsh=128, k=DUMMY, v=DUMMY, nb=100, csb=16 * 8 * 128, cst=8 * 128, csh=128,
+             bt=DUMMY, bts=4, btw=4, ctx=DUMMY, out=DUMMY, osb=32 * 128, osh=128, ws=None, wsb=0, b=2, h=32,
+             kv=8, d=128, bs=16, maxc=64, scale=0.1, dt=1, stream=None)
+    a.update(kw)
+    return _lib.load().nimbus_paged_decode(*a.values())
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(bs=8), _lib.NIMBUS_ERR_UNSUPPORTED),
+    (dict(d=96), _lib.NIMBUS_ERR_UNSUPPORTED),
+    (dict(dt=7), _lib.NIMBUS_ERR_UNSUPPORTED),
+    (dict(h=30), _lib.NIMBUS_ERR_INVALID),
+    (dict(q=None), _lib.NIMBUS_ERR_INVALID),
+    (dict(qsh=100), _lib.NIMBUS_ERR_ALIGNMENT),
+    (dict(q=DUMMY + 2), _lib.NIMBUS_ERR_ALIGNMENT),
+    (dict(maxc=4096), _lib.NIMBUS_ERR_WORKSPACE),
+    (dict(b=0), 0),
+    (dict(maxc=0), 0),
+])
+def test_decode_argument_checks(kw, code):
+    assert _decode(**kw) == code
+
+
+def test_prefill_and_write_kv_argument_checks():
+    lib = _lib.load()
+    base = [DUMMY, 32 * 128, 128, DUMMY, DUMMY, 100, 16 * 8 * 128, 8 * 128, 128, DUMMY, 4, 4, DUMMY, DUMMY, DUMMY,
+            DUMMY, 3, DUMMY, 32 * 128, 128, 32, 8, 128, 16, 0.1, 1, None]
+    assert lib.nimbus_paged_prefill(*base[:23], 8, *base[24:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # block size
+    assert lib.nimbus_paged_prefill(*base[:16], 0, *base[17:]) == 0  # no tiles: nothing to launch
+    assert lib.nimbus_paged_prefill(*base[:22], 80, *base[23:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # head dim
+    wk = [DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 0, 8, 128, 8 * 128, 128, 8 * 128, 128, 1600, 1, None]
+    assert lib.nimbus_write_kv(*wk) == 0  # zero tokens
+    wk[13] = 3
+    wk[5] = 5
+    assert lib.nimbus_write_kv(*wk) == _lib.NIMBUS_ERR_UNSUPPORTED

@@ -1,0 +1,90 @@
+"""GPU: the drop-in backend (write -> prefill -> decode on one flat batch) and
+decode attention replayed from hipGraphs at padded batch sizes."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nimbus_amd import workloads
+from nimbus_amd.graphs import DecodeAttentionGraphs
+from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
+from tests.gpu_helpers import announce, oracle_decode, oracle_prefill
+from tests.helpers import assert_within
+
+pytestmark = pytest.mark.gpu
+
+
+def _meta(b: workloads.PagedBatch) -> AttnMetadata:
+    p = b.num_prefills
+    pa = b.prefill_args()
+    da = b.decode_args()
+    return AttnMetadata(
+        slot_mapping=b.slot_mapping, num_prefill_tokens=b.num_prefill_tokens, prefill_query_start=pa[3],
+        prefill_context_lens=pa[4], prefill_block_tables=b.block_tables[:p], decode_context_lens=da[3],
+        decode_block_tables=da[4], max_decode_context=da[5], prefill_query_start_host=pa[7],
+        prefill_context_lens_host=pa[8])
+
+
+def test_mixed_step_matches_oracle():
+    """BASELINE config 4 layout: 4 prefill chunks of 512 over cached prefixes,
+    then 60 decodes, flat and prefill-first; the backend writes the new K/V
+    first (write_first=False here so the backend's own write is what counts)."""
+    announce("backend mixed step (llama3_mixed)")
+    b = workloads.llama3_mixed("cuda")
+    # Rebuild with the new tokens NOT yet in the cache.
+    b = workloads.build_batch(b.seqs, heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16, device="cuda",
+                              seed=0, write_first=False)
+    k_before = b.k_cache.clone()
+    out = AttentionBackend().forward(b.q, b.k, b.v, b.k_cache, b.v_cache, _meta(b), b.scale)
+    torch.cuda.synchronize()
+    # the slot write is bit-exact
+    kref = k_before.view(-1, 8, 128)
+    kref[b.slot_mapping] = b.k
+    assert torch.equal(b.k_cache.view(-1, 8, 128).view(torch.int16), kref.view(torch.int16))
+    p = b.num_prefill_tokens
+    q, k, v, _, _, bt, scale, qs, ctx = b.prefill_args()
+    assert_within(out[:p].cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="prefill part")
+    da = b.decode_args()
+    assert_within(out[p:].cpu(), oracle_decode(da[0], b.k_cache, b.v_cache, b.decode_context_host(), da[4], scale),
+                  what="decode part")
+
+
+@pytest.mark.parametrize("n", [60, 3, 1])
+def test_decode_graph_replay_matches_eager(n):
+    """Decode attention captured at padded sizes (padding rows on a scratch
+    block) equals the eager call on the real rows; every replay, with eager
+    work and synchronisations between replays, gives the same result."""
+    announce(f"graph replay n={n}")
+    ctx = workloads.llama3_decode_lens(seed=n, batch=n)
+    b = workloads.build_batch([(c, 1) for c in ctx], heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16,
+                              device="cuda", seed=n, pool_factor=1.3, write_first=False)
+    nb = b.k_cache.shape[0]
+    # one extra block that no sequence owns absorbs the padding rows
+    kc = torch.cat([b.k_cache, torch.zeros_like(b.k_cache[:1])])
+    vc = torch.cat([b.v_cache, torch.zeros_like(b.v_cache[:1])])
+    graphs = DecodeAttentionGraphs(kc, vc, num_heads=32, scale=b.scale, max_model_len=8192, max_batch=64,
+                                   scratch_block=nb)
+    graphs.capture()
+    da = b.decode_args()
+    k_new = torch.randn(n, 8, 128, device="cuda").bfloat16()
+    v_new = torch.randn(n, 8, 128, device="cuda").bfloat16()
+    # decode writes its token's K/V at position ctx-1 first
+    slots = torch.tensor([t[(c - 1) // 16] * 16 + (c - 1) % 16 for t, c in zip(b.tables_host, ctx)],
+                         dtype=torch.int64, device="cuda")
+    kc_e, vc_e = kc.clone(), vc.clone()
+    eager_meta = AttnMetadata(
+        slot_mapping=slots, num_prefill_tokens=0,
+        prefill_query_start=torch.zeros(1, dtype=torch.int32, device="cuda"),
+        prefill_context_lens=torch.zeros(0, dtype=torch.int32, device="cuda"),
+        prefill_block_tables=torch.zeros(0, 1, dtype=torch.int32, device="cuda"),
+        decode_context_lens=da[3], decode_block_tables=da[4], max_decode_context=da[5],
+        prefill_query_start_host=[0], prefill_context_lens_host=[])
+    eager = AttentionBackend().forward(da[0], k_new, v_new, kc_e, vc_e, eager_meta, b.scale)
+    for rep in range(3):
+        got = graphs.run(da[0], k_new, v_new, slots, da[3], da[4]).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager), f"replay {rep}"
+        _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # eager work between replays
+    assert torch.equal(kc[:nb], kc_e[:nb]) and torch.equal(vc[:nb], vc_e[:nb])
+    assert_within(eager.cpu(), oracle_decode(da[0], kc_e, vc_e, ctx, da[4], b.scale), what="eager vs oracle")

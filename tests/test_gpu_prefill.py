@@ -1,0 +1,95 @@
+"""GPU: causal varlen paged prefill matches the oracle within the bar.
+
+Covers the reference's test matrix (tests/test_kernels.py:54-75 of Nimbus:
+fresh prompts across 64-query tile edges, cached prefixes, a single token)
+plus bf16, D=128, GQA groups 1..8, long chunks over long prefixes, and the
+two prefill configurations at full size.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nimbus_amd import workloads
+from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
+from oracle import closed_form
+from tests import golden_io
+from tests.gpu_helpers import announce, oracle_prefill
+from tests.helpers import assert_within, query_starts, random_tables, scattered_cache
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(heads, kv, d, seqs, dtype, seed=1, pool=None):
+    ctx_lens = [c for _, c in seqs]
+    pool = pool or max(64, sum(-(-c // 16) for c in ctx_lens) + 8)
+    k, v = scattered_cache(pool, 16, kv, d, seed=seed, dtype=dtype, device="cuda")
+    bt = random_tables(ctx_lens, 16, pool, seed=seed, device="cuda")
+    qs = query_starts([ql for ql, _ in seqs])
+    g = torch.Generator(device="cuda").manual_seed(seed + 2)
+    q = torch.randn(qs[-1], heads, d, generator=g, device="cuda").to(dtype)
+    args = (q, k, v, torch.tensor(qs, dtype=torch.int32, device="cuda"),
+            torch.tensor(ctx_lens, dtype=torch.int32, device="cuda"), bt, d ** -0.5, qs, ctx_lens)
+    return args
+
+
+REF_SEQS = [[(5, 5), (64, 64), (130, 130)], [(3, 40), (17, 17), (1, 9), (70, 200)], [(1, 1)]]
+
+
+@pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8)])
+@pytest.mark.parametrize("seqs", REF_SEQS)
+def test_reference_matrix_fp16_d64(heads, kv, seqs):
+    announce(f"prefill ref-matrix H={heads} KV={kv} seqs={seqs}")
+    args = _case(heads, kv, 64, seqs, torch.float16, pool=400)
+    got = paged_prefill_attention(*args)
+    q, k, v, _, _, bt, scale, qs, ctx = args
+    want = oracle_prefill(q, k, v, qs, ctx, bt, scale)
+    assert_within(got.cpu(), want, what="vs oracle")
+    assert_within(got.cpu(), closed_form.prefill(q.cpu(), k.cpu(), v.cpu(), qs, ctx, bt.cpu(), scale),
+                  what="vs float64")
+
+
+SEQS = [(1, 1), (64, 64), (65, 65), (3, 700), (130, 1000), (512, 1536), (200, 201)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("heads,kv,d", [(32, 8, 128), (32, 4, 64), (32, 4, 128), (8, 8, 64), (12, 4, 64),
+                                        (32, 16, 128), (16, 2, 64)])
+def test_group_sizes_dtypes_and_long_chunks(dtype, heads, kv, d):
+    announce(f"prefill H={heads} KV={kv} D={d} {dtype}")
+    args = _case(heads, kv, d, SEQS, dtype, seed=4)
+    got = paged_prefill_attention(*args)
+    q, k, v, _, _, bt, scale, qs, ctx = args
+    assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="vs oracle")
+
+
+def test_prebuilt_programs_and_out_slice():
+    announce("prefill programs + out slice")
+    seqs = [(70, 90), (5, 5)]
+    q, k, v, qst, ctxt, bt, scale, qs, ctx = _case(32, 8, 128, seqs, torch.bfloat16, seed=6)
+    progs = build_programs(qs, "cuda")
+    flat = torch.full((qs[-1] + 3, 32, 128), 5.0, device="cuda").bfloat16()
+    paged_prefill_attention(q, k, v, qst, ctxt, bt, scale, qs, ctx, progs, out=flat[:qs[-1]])
+    assert flat[qs[-1]:].eq(5).all()
+    assert_within(flat[:qs[-1]].cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="vs oracle")
+
+
+@pytest.mark.parametrize("name", golden_io.names("prefill"))
+def test_golden_fixture(name):
+    announce(f"prefill golden {name}")
+    f = golden_io.load(name, device="cuda")
+    qs = f["query_start"].tolist()
+    got = paged_prefill_attention(f["q"], f["k_cache"], f["v_cache"], f["query_start"], f["context_lens"],
+                                  f["block_tables"], f["scale"], qs, f["context_lens"].tolist())
+    assert_within(got.cpu(), f["out"], what=name)
+
+
+@pytest.mark.parametrize("config", ["tinyllama_prefill", "llama3_mixed"])
+def test_prefill_configs_full(config):
+    announce(f"prefill config {config}")
+    b = workloads.CONFIGS[config]("cuda")
+    args = b.prefill_args()
+    got = paged_prefill_attention(*args)
+    q, k, v, _, _, bt, scale, qs, ctx = args
+    assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what=config)

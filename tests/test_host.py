@@ -1,0 +1,110 @@
+"""CPU: host-side logic of the boundary (tile table, metadata, workloads,
+algorithmic work formulas) and the absence of any CPU fallback."""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+
+import pytest
+import torch
+
+from nimbus_amd import workloads
+from nimbus_amd.kernels import cache_ops, paged_attention, prefill_attention
+from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
+
+
+def _programs_loop(query_start_host, block_m=64):
+    """The reference's build_programs loop (prefill_attention.py:81-90), restated."""
+    seqs, starts = [], []
+    for i in range(len(query_start_host) - 1):
+        q_len = query_start_host[i + 1] - query_start_host[i]
+        for m0 in range(0, q_len, block_m):
+            seqs.append(i)
+            starts.append(m0)
+    return seqs, starts
+
+
+@pytest.mark.parametrize("qs", [[0], [0, 1], [0, 64], [0, 65], [0, 5, 69, 72, 72, 202], [0, 512, 1024, 1600]])
+def test_build_programs_matches_reference_loop(qs):
+    s, m = prefill_attention.build_programs(qs, "cpu")
+    want_s, want_m = _programs_loop(qs)
+    assert s.tolist() == want_s and m.tolist() == want_m
+    assert s.dtype == m.dtype == torch.int32
+
+
+def test_attn_metadata_fields_match_reference():
+    # nimbus/model/attention.py:24-50, in order
+    want = ["slot_mapping", "num_prefill_tokens", "prefill_query_start", "prefill_context_lens",
+            "prefill_block_tables", "decode_context_lens", "decode_block_tables", "max_decode_context",
+            "prefill_query_start_host", "prefill_context_lens_host", "prefill_programs", "decode_partitions"]
+    assert [f.name for f in dataclasses.fields(AttnMetadata)] == want
+
+
+def test_backend_has_no_cpu_path():
+    with pytest.raises(ValueError):
+        AttentionBackend(False)
+
+
+def test_kernels_refuse_cpu_tensors():
+    k = torch.zeros(4, 16, 2, 64, dtype=torch.float16)
+    q = torch.zeros(2, 4, 64, dtype=torch.float16)
+    ctx = torch.ones(2, dtype=torch.int32)
+    bt = torch.zeros(2, 1, dtype=torch.int32)
+    with pytest.raises(ValueError, match="GPU"):
+        paged_attention.paged_decode_attention(q, k, k, ctx, bt, 1, 0.125)
+    with pytest.raises(ValueError, match="GPU"):
+        prefill_attention.paged_prefill_attention(q, k, k, torch.tensor([0, 2], dtype=torch.int32), ctx[:1],
+                                                  bt[:1], 0.125, [0, 2], [2])
+    with pytest.raises(ValueError, match="GPU"):
+        cache_ops.write_kv(q[:, :2], q[:, :2], k, k, torch.zeros(2, dtype=torch.int64))
+
+
+def test_batch_layout_follows_runner():
+    b = workloads.build_batch([(40, 40), (70, 30), (100, 1), (17, 1)], heads=4, kv_heads=2, head_dim=64,
+                              dtype=torch.float16, device="cpu", seed=3)
+    assert b.num_prefills == 2 and b.num_prefill_tokens == 70
+    # slot formula nimbus/runner.py:61
+    slots = []
+    for (c, ql), t in zip(b.seqs, b.tables_host):
+        slots += [t[p // 16] * 16 + p % 16 for p in range(c - ql, c)]
+    assert b.slot_mapping.tolist() == slots
+    # zero-padded tables (runner.py:24-30)
+    assert b.block_tables.shape == (4, 7)
+    assert b.block_tables[3, 2:].eq(0).all()
+    # the new tokens are in the cache (write first)
+    kc = b.k_cache.view(-1, 2, 64)
+    assert torch.equal(kc[b.slot_mapping], b.k)
+    pa = b.prefill_args()
+    assert pa[7] == [0, 40, 70] and pa[8] == [40, 70]
+    da = b.decode_args()
+    assert da[5] == 100 and da[0].shape == (2, 4, 64)
+
+
+def test_pages_are_distinct():
+    b = workloads.tinyllama_decode("cpu")
+    pages = [p for t in b.tables_host for p in t]
+    assert len(pages) == len(set(pages)) and max(pages) < 1100
+
+
+def test_config_generators_shapes():
+    assert len(workloads.llama3_decode_lens()) == 64
+    lens = workloads.llama3_decode_lens()
+    assert min(lens) >= 128 and max(lens) <= 8192
+    long_ = workloads.llama3_long_lens()
+    assert len(long_) == 256 and max(long_) <= 32768
+    assert sum(c >= 16384 for c in long_) >= 10
+
+
+def test_decode_bytes_formula():
+    # sum ctx * 2 * KV * D * 2 + 2 * B * H * D * 2 + 4 * sum pages + 4 * B
+    assert workloads.decode_bytes([512], 32, 4, 64) == 512 * 2 * 4 * 64 * 2 + 2 * 32 * 64 * 2 + 4 * 32 + 4
+    assert workloads.decode_bytes([1, 17], 32, 8, 128) == 18 * 4096 + 2 * 2 * 32 * 128 * 2 + 4 * 3 + 8
+
+
+def test_prefill_flops_formula():
+    # fresh prompt of n: 4*D*H*n(n+1)/2
+    assert workloads.prefill_flops([(512, 512)], 32, 64) == 4 * 64 * 32 * 512 * 513 // 2
+    # 3 new on a prefix of 37: 3*37 + 3*4/2 pairs
+    assert workloads.prefill_flops([(40, 3)], 1, 1) == 4 * (3 * 37 + 6)
+    assert math.isclose(workloads.prefill_flops([(40, 3)], 2, 2), 4 * 4 * 117)

@@ -1,0 +1,257 @@
+"""Pins the CPU oracle (oracle/reference.py) before anything is checked against it.
+
+Three independent pins, chosen so a plausible slip fails at least one:
+  1. float64 NumPy brute force (oracle/closed_form.py), written from the
+     definition rather than through torch's gather + SDPA;
+  2. textbook special cases: ctx == 1 returns v_0; a zero query averages V;
+     a one-hot score selects one row of V; the last query of a fresh prompt
+     equals decode over the same context; query 0 of a fresh prompt is v_0;
+  3. planted mistakes (wrong GQA head map, off-by-one masks, dropped scale,
+     reversed pages, V/K swapped, prefix ignored) must each be caught.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import closed_form, reference
+from tests.helpers import assert_within, max_violation, query_starts, random_tables, scattered_cache
+
+BS = 16
+
+
+def _decode_inputs(heads, kv, d, ctx_lens, dtype=torch.float32, seed=0, pool=400):
+    k, v = scattered_cache(pool, BS, kv, d, seed=seed, dtype=dtype)
+    bt = random_tables(ctx_lens, BS, pool, seed=seed)
+    g = torch.Generator().manual_seed(seed + 7)
+    q = torch.randn(len(ctx_lens), heads, d, generator=g).to(dtype)
+    ctx = torch.tensor(ctx_lens, dtype=torch.int32)
+    return q, k, v, ctx, bt, d ** -0.5
+
+
+def _prefill_inputs(heads, kv, d, seqs, dtype=torch.float32, seed=1, pool=400):
+    k, v = scattered_cache(pool, BS, kv, d, seed=seed, dtype=dtype)
+    ctx_lens = [c for _, c in seqs]
+    bt = random_tables(ctx_lens, BS, pool, seed=seed)
+    qs = query_starts([ql for ql, _ in seqs])
+    g = torch.Generator().manual_seed(seed + 11)
+    q = torch.randn(qs[-1], heads, d, generator=g).to(dtype)
+    return (q, k, v, torch.tensor(qs, dtype=torch.int32), torch.tensor(ctx_lens, dtype=torch.int32), bt, d ** -0.5,
+            qs, ctx_lens)
+
+
+DECODE_CASES = [
+    (32, 4, 64, [1, 17, 64, 100, 255, 300]),
+    (8, 8, 64, [700, 33]),
+    (32, 8, 128, [1, 129, 511, 1000]),
+    (12, 4, 64, list(range(1, 200, 37))),
+]
+PREFILL_CASES = [
+    (32, 4, 64, [(5, 5), (64, 64), (130, 130)]),
+    (8, 8, 64, [(3, 40), (17, 17), (1, 9), (70, 200)]),
+    (32, 8, 128, [(1, 1), (33, 100)]),
+]
+
+
+# ---------------------------------------------------------------- pin 1: float64 brute force
+
+@pytest.mark.parametrize("heads,kv,d,ctx_lens", DECODE_CASES)
+def test_decode_oracle_matches_float64_brute_force(heads, kv, d, ctx_lens):
+    q, k, v, ctx, bt, scale = _decode_inputs(heads, kv, d, ctx_lens)
+    got = reference.paged_decode_attention(q, k, v, ctx, bt, max(ctx_lens), scale)
+    want = closed_form.decode(q, k, v, ctx, bt, scale)
+    np.testing.assert_allclose(got.double().numpy(), want, atol=2e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_oracle_low_precision_within_bar(dtype):
+    q, k, v, ctx, bt, scale = _decode_inputs(32, 8, 128, [1, 77, 300, 1024], dtype=dtype)
+    got = reference.paged_decode_attention(q, k, v, ctx, bt, 1024, scale)
+    assert_within(got, closed_form.decode(q, k, v, ctx, bt, scale), what=f"oracle {dtype}")
+
+
+@pytest.mark.parametrize("heads,kv,d,seqs", PREFILL_CASES)
+def test_prefill_oracle_matches_float64_brute_force(heads, kv, d, seqs):
+    args = _prefill_inputs(heads, kv, d, seqs)
+    q, k, v, _, _, bt, scale, qs, ctx_lens = args
+    got = reference.paged_prefill_attention(*args)
+    want = closed_form.prefill(q, k, v, qs, ctx_lens, bt, scale)
+    np.testing.assert_allclose(got.double().numpy(), want, atol=2e-5, rtol=1e-4)
+
+
+def test_decode_rows_form_equals_batched_form():
+    q, k, v, ctx, bt, scale = _decode_inputs(32, 4, 64, [5, 300, 17, 1024])
+    a = reference.paged_decode_attention(q, k, v, ctx, bt, 1024, scale)
+    b = reference.decode_attention_rows(q, k, v, ctx.tolist(), bt, scale)
+    torch.testing.assert_close(a, b, atol=1e-6, rtol=1e-5)
+
+
+def test_gather_matches_slot_rule():
+    k, _ = scattered_cache(50, BS, 2, 8, seed=3)
+    bt = random_tables([37], BS, 50, seed=3)
+    got = reference.gather_kv(k, bt[0], 37).numpy()
+    want = closed_form.token_rows(k, bt[0], 37)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_write_kv_oracle_is_a_bitwise_scatter(dtype):
+    kc, vc = scattered_cache(30, BS, 4, 64, seed=5, dtype=dtype)
+    g = torch.Generator().manual_seed(5)
+    slots = torch.randperm(30 * BS, generator=g)[:77].to(torch.int64)
+    k = torch.randn(77, 4, 64, generator=g).to(dtype)
+    v = torch.randn(77, 4, 64, generator=g).to(dtype)
+    want_k, want_v = closed_form.write_kv(k.view(torch.int16), v.view(torch.int16), kc.view(torch.int16),
+                                          vc.view(torch.int16), slots)
+    reference.write_kv(k, v, kc, vc, slots)
+    np.testing.assert_array_equal(kc.view(torch.int16).numpy(), want_k)
+    np.testing.assert_array_equal(vc.view(torch.int16).numpy(), want_v)
+
+
+def test_write_then_gather_roundtrip():
+    """Tokens written at slot table[p // 16] * 16 + p % 16 (nimbus/runner.py:61)
+    come back from gather_kv at position p."""
+    kc, vc = scattered_cache(40, BS, 2, 16, seed=9, dtype=torch.float32)
+    bt = random_tables([70], BS, 40, seed=9)
+    table = bt[0].tolist()
+    pos = torch.arange(20, 70)
+    slots = torch.tensor([table[p // BS] * BS + p % BS for p in pos.tolist()], dtype=torch.int64)
+    k = torch.randn(50, 2, 16)
+    reference.write_kv(k, k.clone(), kc, vc, slots)
+    torch.testing.assert_close(reference.gather_kv(kc, bt[0], 70)[20:70], k, atol=0, rtol=0)
+
+
+# ---------------------------------------------------------------- pin 2: textbook special cases
+
+@pytest.mark.parametrize("impl", ["reference", "closed_form"])
+def test_context_of_one_returns_first_value_row(impl):
+    q, k, v, ctx, bt, scale = _decode_inputs(8, 2, 64, [1, 1, 1])
+    out = _decode(impl, q, k, v, ctx, bt, scale)
+    for b in range(3):
+        page = int(bt[b, 0])
+        want = v[page, 0].double().repeat_interleave(4, 0).numpy()  # head h uses kv head h // 4
+        np.testing.assert_allclose(out[b], want, atol=1e-6)
+
+
+@pytest.mark.parametrize("impl", ["reference", "closed_form"])
+def test_zero_query_averages_values(impl):
+    q, k, v, ctx, bt, scale = _decode_inputs(8, 2, 32, [40, 7])
+    q.zero_()
+    out = _decode(impl, q, k, v, ctx, bt, scale)
+    for b, c in enumerate([40, 7]):
+        rows = closed_form.token_rows(v, bt[b], c)  # [c, KV, D]
+        want = rows.mean(axis=0).repeat(4, axis=0)
+        np.testing.assert_allclose(out[b], want, atol=1e-5)
+
+
+@pytest.mark.parametrize("impl", ["reference", "closed_form"])
+def test_one_hot_score_selects_one_value_row(impl):
+    heads, kv, d, c = 4, 2, 16, 45
+    q, k, v, ctx, bt, _ = _decode_inputs(heads, kv, d, [c])
+    k.zero_()
+    j = 29  # the selected token
+    page, row = int(bt[0, j // BS]), j % BS
+    k[page, row, :, 0] = 1.0
+    q.zero_()
+    q[0, :, 0] = 1000.0
+    out = _decode(impl, q, k, v, ctx, bt, 1.0)
+    want = v[page, row].double().repeat_interleave(2, 0).numpy()
+    np.testing.assert_allclose(out[0], want, atol=1e-6)
+
+
+@pytest.mark.parametrize("impl", ["reference", "closed_form"])
+def test_fresh_prompt_first_query_sees_only_first_key(impl):
+    args = _prefill_inputs(8, 2, 64, [(50, 50)])
+    out = _prefill(impl, args)
+    page = int(args[5][0, 0])
+    want = args[2][page, 0].double().repeat_interleave(4, 0).numpy()
+    np.testing.assert_allclose(out[0], want, atol=1e-6)
+
+
+@pytest.mark.parametrize("impl", ["reference", "closed_form"])
+def test_last_prefill_query_equals_decode_over_same_context(impl):
+    args = _prefill_inputs(8, 2, 64, [(30, 95)])
+    q, k, v, _, ctx, bt, scale, _, _ = args
+    pre = _prefill(impl, args)
+    dec = _decode(impl, q[-1:], k, v, ctx, bt, scale)
+    np.testing.assert_allclose(pre[-1], dec[0], atol=1e-6)
+
+
+def _decode(impl, q, k, v, ctx, bt, scale):
+    if impl == "reference":
+        return reference.paged_decode_attention(q, k, v, ctx, bt, int(ctx.max()), scale).double().numpy()
+    return closed_form.decode(q, k, v, ctx, bt, scale)
+
+
+def _prefill(impl, args):
+    if impl == "reference":
+        return reference.paged_prefill_attention(*args).double().numpy()
+    q, k, v, _, _, bt, scale, qs, ctx_lens = args
+    return closed_form.prefill(q, k, v, qs, ctx_lens, bt, scale)
+
+
+# ---------------------------------------------------------------- pin 3: planted mistakes are caught
+
+def _mutant_decode(kind, q, k_cache, v_cache, context_lens, block_tables, max_context, scale):
+    """oracle.reference.paged_decode_attention with one planted mistake."""
+    b, h, d = q.shape
+    kv = k_cache.shape[2]
+    nb = -(-max_context // BS)
+    bt = block_tables[:, :nb].long()
+    if kind == "reversed_pages":
+        bt = bt.flip(1)
+    k = k_cache[bt].flatten(1, 2).transpose(1, 2)
+    v = v_cache[bt].flatten(1, 2).transpose(1, 2)
+    if kind == "swap_kv":
+        v = k
+    if kind == "gqa_modulo":
+        k = k.repeat(1, h // kv, 1, 1)
+        v = v.repeat(1, h // kv, 1, 1)
+    else:
+        k = k.repeat_interleave(h // kv, 1)
+        v = v.repeat_interleave(h // kv, 1)
+    lim = context_lens[:, None] - (1 if kind == "mask_off_by_one" else 0)
+    mask = torch.arange(k.shape[2])[None, :] < lim
+    s = 1.0 if kind == "no_scale" else scale
+    o = F.scaled_dot_product_attention(q.unsqueeze(2), k, v, attn_mask=mask[:, None, None, :], scale=s)
+    return o.view(b, h, d)
+
+
+@pytest.mark.parametrize("kind", ["reversed_pages", "swap_kv", "gqa_modulo", "mask_off_by_one", "no_scale"])
+def test_planted_decode_mistakes_are_caught(kind):
+    q, k, v, ctx, bt, scale = _decode_inputs(32, 4, 64, [2, 17, 100, 300])
+    want = closed_form.decode(q, k, v, ctx, bt, scale)
+    good = reference.paged_decode_attention(q, k, v, ctx, bt, 300, scale)
+    assert max_violation(good, want) <= 0
+    bad = _mutant_decode(kind, q, k, v, ctx, bt, 300, scale)
+    assert not (max_violation(torch.nan_to_num(bad, nan=1e9), want) <= 0), kind
+
+
+def _mutant_prefill(kind, q, k_cache, v_cache, qs, ctx_lens, bt, scale):
+    out = torch.empty_like(q)
+    for i, ctx in enumerate(ctx_lens):
+        s, e = qs[i], qs[i + 1]
+        ql = e - s
+        qi = q[s:e].transpose(0, 1).unsqueeze(0)
+        ki = reference.gather_kv(k_cache, bt[i], ctx).transpose(0, 1).unsqueeze(0)
+        vi = reference.gather_kv(v_cache, bt[i], ctx).transpose(0, 1).unsqueeze(0)
+        base = 0 if kind == "ignores_prefix" else ctx - ql
+        qpos = torch.arange(base, base + ql)[:, None]
+        kpos = torch.arange(ctx)[None, :]
+        allowed = kpos < qpos if kind == "strict_causal" else kpos <= qpos
+        o = F.scaled_dot_product_attention(qi, ki, vi, attn_mask=allowed, scale=scale, enable_gqa=True)
+        out[s:e] = o[0].transpose(0, 1)
+    return out
+
+
+@pytest.mark.parametrize("kind", ["strict_causal", "ignores_prefix"])
+def test_planted_prefill_mistakes_are_caught(kind):
+    args = _prefill_inputs(8, 2, 64, [(3, 40), (17, 17), (70, 200)])
+    q, k, v, _, _, bt, scale, qs, ctx_lens = args
+    want = closed_form.prefill(q, k, v, qs, ctx_lens, bt, scale)
+    assert max_violation(reference.paged_prefill_attention(*args), want) <= 0
+    bad = _mutant_prefill(kind, q, k, v, qs, ctx_lens, bt, scale)
+    assert not (max_violation(torch.nan_to_num(bad, nan=1e9), want) <= 0), kind
