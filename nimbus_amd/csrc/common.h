@@ -52,6 +52,35 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return x;
 }
 
+// The P.V product of both attention kernels runs in fp16 whatever the cache
+// dtype: P lies in [0, 1], where fp16 keeps 3 more mantissa bits than bf16
+// (rounding P to bf16 alone costs ~8e-3 at |o| ~ 0.5, beyond the output
+// tolerance), and a bf16 V element converts to fp16 exactly when
+// |v| <= 65504 (smaller magnitudes lose at most 2^-25 in fp16's subnormal
+// range). Larger |v| saturate to +-65504 rather than becoming inf, so one
+// outlier cannot turn masked-out products (0 * inf) into NaN for other rows.
+template <int DT>
+__device__ __forceinline__ uint16_t v_to_f16_bits(uint16_t x);
+
+template <>
+__device__ __forceinline__ uint16_t v_to_f16_bits<kFloat16>(uint16_t x) {
+  return x;
+}
+
+template <>
+__device__ __forceinline__ uint16_t v_to_f16_bits<kBFloat16>(uint16_t x) {
+  float f = bf16_to_f32(x);
+  if (__builtin_fabsf(f) > 65504.f) f = __builtin_copysignf(65504.f, f);
+  return f32_to_f16(f);
+}
+
+// Two 16-bit V elements packed in a dword, converted together.
+template <int DT>
+__device__ __forceinline__ uint32_t v_to_f16_pair(uint32_t w) {
+  return static_cast<uint32_t>(v_to_f16_bits<DT>(static_cast<uint16_t>(w & 0xffffu))) |
+         (static_cast<uint32_t>(v_to_f16_bits<DT>(static_cast<uint16_t>(w >> 16))) << 16);
+}
+
 template <int DT> struct Elem;
 
 template <> struct Elem<kFloat16> {

@@ -17,8 +17,9 @@
 //                                               HBM into the A-operand layout)
 //   online softmax per column g in fp32 (exp2 domain), reductions across the
 //   four 16-lane groups with lane shuffles
-//   O^T[d][g]    += V^T[d][token] . P^T[token][g]  (16x16x16 MFMA; P^T is the
-//                                               QK output layout as is; V is
+//   O^T[d][g]    += V^T[d][token] . P^T[token][g]  (16x16x16 fp16 MFMA; P^T
+//                                               is the QK output layout as is;
+//                                               V is converted to fp16 while
 //                                               staged through LDS, read
 //                                               transposed)
 // The four waves' partial (m, l, O) are merged through LDS. A sequence that
@@ -171,6 +172,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
       const int tt = r * TPL + lane / LPT;
       const int cc = lane % LPT;
       u32x4 v = tt < valid ? vreg[r] : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = v_to_f16_pair<DT>(v[e]);
       u32x2* dst = reinterpret_cast<u32x2*>(vb + tt * VROW + 8 * cc);
       dst[0] = u32x2{v[0], v[1]};
       dst[1] = u32x2{v[2], v[3]};
@@ -212,8 +215,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
         p[r] = exp2f(s[pi][r] - m_new);
         psum += p[r];
       }
-      pop[pi] = u32x2{pack2(Elem<DT>::from_f32(p[0]), Elem<DT>::from_f32(p[1])),
-                      pack2(Elem<DT>::from_f32(p[2]), Elem<DT>::from_f32(p[3]))};
+      pop[pi] = u32x2{pack2(f32_to_f16(p[0]), f32_to_f16(p[1])), pack2(f32_to_f16(p[2]), f32_to_f16(p[3]))};
     }
     l_run = l_run * alpha + psum;
 #pragma unroll
@@ -229,7 +231,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs
       for (int nn = 0; nn < NN; ++nn) {
         const uint16_t* p = vrow + 16 * nn;
         u32x2 vop = u32x2{pack2(p[0], p[VROW]), pack2(p[2 * VROW], p[3 * VROW])};
-        acc[nn] = mfma_16x16x16<DT>(vop, pop[pi], acc[nn]);
+        acc[nn] = mfma_16x16x16<kFloat16>(vop, pop[pi], acc[nn]);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

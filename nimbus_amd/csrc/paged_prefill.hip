@@ -17,8 +17,10 @@
 // V^T[d][key]) in LDS, then each wave computes
 //   S^T[key][row] = K[key][:] . Q^T[:][row]    16x16x32 MFMA, Q^T in registers
 //   online softmax per row in fp32 (exp2 domain)
-//   O^T[d][row]  += V^T[d][key] . P^T[key][row] 16x16x32 MFMA; P^T is the QK
-//                                               output layout as is
+//   O^T[d][row]  += V^T[d][key] . P^T[key][row] 16x16x32 fp16 MFMA; P^T is
+//                                               the QK output layout as is,
+//                                               V^T is converted to fp16 when
+//                                               staged
 // Waves skip key blocks that lie entirely after their last query position.
 #include "common.h"
 #include "nimbus_attn_internal.h"
@@ -159,7 +161,9 @@ __global__ __launch_bounds__(128 * GS) void paged_prefill_kernel(PrefillArgs a) 
       const int key = p / (D / 8);
       const int dc = p % (D / 8);
       *reinterpret_cast<u32x4*>(ks + key * KROW + 8 * dc) = kreg[i];
-      const u32x4 v = vreg[i];
+      u32x4 v = vreg[i];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = v_to_f16_pair<DT>(v[e]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         vts[(8 * dc + 2 * e) * VROW + key] = static_cast<uint16_t>(v[e] & 0xffffu);
@@ -214,7 +218,7 @@ __global__ __launch_bounds__(128 * GS) void paged_prefill_kernel(PrefillArgs a) 
         for (int r = 0; r < 4; ++r) {
           const float p = exp2f(s[mb][nb][r] - m_safe);
           psum += p;
-          ph[mb][r] = Elem<DT>::from_f32(p);
+          ph[mb][r] = f32_to_f16(p);
         }
       }
       l_run[nb] = l_run[nb] * alpha + psum;
@@ -236,8 +240,8 @@ __global__ __launch_bounds__(128 * GS) void paged_prefill_kernel(PrefillArgs a) 
         const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow + 32 * kc + 4 * grp);
         const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 32 * kc + 16 + 4 * grp);
         const u32x4 vop = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        acc[nd][0] = mfma_16x16x32<DT>(vop, pop[kc][0], acc[nd][0]);
-        acc[nd][1] = mfma_16x16x32<DT>(vop, pop[kc][1], acc[nd][1]);
+        acc[nd][0] = mfma_16x16x32<kFloat16>(vop, pop[kc][0], acc[nd][0]);
+        acc[nd][1] = mfma_16x16x32<kFloat16>(vop, pop[kc][1], acc[nd][1]);
       }
     }
   }

@@ -42,7 +42,10 @@ def test_reference_matrix_fp16_d64(heads, kv, ctx_lens):
     q, k, v, ctx, bt, scale = _case(heads, kv, 64, ctx_lens, torch.float16, pool=800)
     got = paged_decode_attention(q, k, v, ctx, bt, max(ctx_lens), scale)
     want = oracle_decode(q, k, v, ctx_lens, bt, scale, batched=True)
-    assert_within(got.cpu(), want, what="vs oracle")
+    assert_within(got.cpu(), want, what="vs oracle (fp32 accumulation)")
+    # fp16, as the reference's own test: the oracle in the input dtype holds too
+    assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale, batched=True, in_dtype=True),
+                  what="vs oracle in fp16")
     assert_within(got.cpu(), closed_form.decode(q.cpu(), k.cpu(), v.cpu(), ctx.cpu(), bt.cpu(), scale),
                   what="vs float64")
 

@@ -45,7 +45,8 @@ def test_reference_matrix_fp16_d64(heads, kv, seqs):
     got = paged_prefill_attention(*args)
     q, k, v, _, _, bt, scale, qs, ctx = args
     want = oracle_prefill(q, k, v, qs, ctx, bt, scale)
-    assert_within(got.cpu(), want, what="vs oracle")
+    assert_within(got.cpu(), want, what="vs oracle (fp32 accumulation)")
+    assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale, in_dtype=True), what="vs oracle in fp16")
     assert_within(got.cpu(), closed_form.prefill(q.cpu(), k.cpu(), v.cpu(), qs, ctx, bt.cpu(), scale),
                   what="vs float64")
 

@@ -72,8 +72,8 @@ def test_write_kv_golden(name):
     f = golden_io.load(name, device="cuda")
     kc, vc = f["k_cache"].clone(), f["v_cache"].clone()
     write_kv(f["k"], f["v"], kc, vc, f["slot_mapping"])
-    assert torch.equal(_bits(kc.cpu()), _bits(f["k_cache_out"]))
-    assert torch.equal(_bits(vc.cpu()), _bits(f["v_cache_out"]))
+    assert torch.equal(_bits(kc.cpu()), _bits(f["k_cache_out"].cpu()))
+    assert torch.equal(_bits(vc.cpu()), _bits(f["v_cache_out"].cpu()))
 
 
 def test_write_kv_empty_batch():

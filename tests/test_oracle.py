@@ -73,6 +73,22 @@ def test_decode_oracle_low_precision_within_bar(dtype):
     assert_within(got, closed_form.decode(q, k, v, ctx, bt, scale), what=f"oracle {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fp32_accumulated_oracle_on_half_inputs_matches_float64(dtype):
+    """The GPU parity checker: the reference ops on fp16/bf16 inputs upcast
+    exactly to fp32 (fp32 accumulation) agree with the float64 brute force to
+    ~1e-6, far inside the output tolerance, for decode and long prefill."""
+    q, k, v, ctx, bt, scale = _decode_inputs(32, 8, 128, [1, 77, 300, 1024, 1500], dtype=dtype)
+    got = reference.paged_decode_attention(q.float(), k.float(), v.float(), ctx, bt, 1500, scale)
+    np.testing.assert_allclose(got.double().numpy(), closed_form.decode(q, k, v, ctx, bt, scale), atol=2e-5,
+                               rtol=1e-4)
+    args = _prefill_inputs(32, 4, 64, [(200, 201), (512, 700), (1, 1)], dtype=dtype)
+    q, k, v, qst, ctxt, bt, scale, qs, ctx_lens = args
+    got = reference.paged_prefill_attention(q.float(), k.float(), v.float(), qst, ctxt, bt, scale, qs, ctx_lens)
+    np.testing.assert_allclose(got.double().numpy(), closed_form.prefill(q, k, v, qs, ctx_lens, bt, scale),
+                               atol=2e-5, rtol=1e-4)
+
+
 @pytest.mark.parametrize("heads,kv,d,seqs", PREFILL_CASES)
 def test_prefill_oracle_matches_float64_brute_force(heads, kv, d, seqs):
     args = _prefill_inputs(heads, kv, d, seqs)
