@@ -56,7 +56,24 @@ def parse(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=25.0, help="bound on the CPU baseline's timed work")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB 5 times (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE/WRITE_SIZE readings to bytes)")
     return ap.parse_args(argv)
+
+
+def copy_calibration(mib):
+    """A plain copy kernel of known size: reads and writes mib MiB per launch."""
+    import torch
+
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 5 copies of {mib} MiB ({mib * 1024} KiB read and written per launch)")
+    del src, dst
 
 
 def log(msg):
@@ -96,7 +113,8 @@ def time_decode(batch, steps, warmup, wall=True):
     import torch
 
     from nimbus_amd import workloads
-    from nimbus_amd.kernels.paged_attention import decode_workspace_bytes, paged_decode_attention
+    from nimbus_amd.kernels.paged_attention import (decode_workspace_bytes, new_decode_workspace,
+                                                    paged_decode_attention)
 
     p = batch.num_prefills
     t0 = batch.num_prefill_tokens
@@ -109,7 +127,7 @@ def time_decode(batch, steps, warmup, wall=True):
     kv = batch.k_cache.shape[2]
     pools = rotated_pools(batch)
     out = torch.empty_like(batch.q[t0:])
-    ws = torch.empty(max(1, decode_workspace_bytes(b, h, d, maxc)), dtype=torch.uint8, device=batch.q.device)
+    ws = new_decode_workspace(decode_workspace_bytes(b, h, d, maxc), batch.q.device)
     stream = torch.cuda.current_stream()
 
     def call(i, entry="nimbus_paged_decode"):
@@ -303,6 +321,8 @@ def main(argv=None):
     _lib.load()
     torch.manual_seed(0)
 
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
     log("building llama3_decode (config 3)")
     batch = workloads.llama3_decode("cuda")
     dec = time_decode(batch, args.steps, args.warmup)

@@ -63,11 +63,18 @@ int nimbus_write_kv(const void* k, const void* v, void* k_cache, void* v_cache, 
                     int32_t dtype, void* stream);
 
 /*
- * Bytes of fp32 workspace nimbus_paged_decode needs for split-context
- * partial results at this batch, head count, head dim and max_context
- * (0 when one partition covers max_context). Pure function of its arguments.
- * Partition size: NIMBUS_DECODE_PARTITION tokens.
+ * Bytes of workspace nimbus_paged_decode needs at this batch, head count,
+ * head dim and max_context: NIMBUS_DECODE_COUNTER_BYTES of work-item
+ * counters, then (when max_context spans more than one partition of
+ * NIMBUS_DECODE_PARTITION tokens) fp32 split-context partial results.
+ * Pure function of its arguments.
+ *
+ * The counter bytes must be zero before a workspace's first use; every
+ * completed call leaves them zero again, so a caller zero-fills a workspace
+ * once, when allocating it. Calls that run concurrently (on different
+ * streams) need different workspaces.
  */
+#define NIMBUS_DECODE_COUNTER_BYTES 256
 #define NIMBUS_DECODE_PARTITION 512
 int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
                                             int64_t max_context);
@@ -80,11 +87,12 @@ int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, in
  * out[b, h, :] = softmax(scale * q[b, h] . K_b^T) V_b over the first
  * context_lens[b] tokens of sequence b, read through block_tables[b] from
  * kv head h / (num_heads / num_kv_heads). q/out: element (b, h, d) at
- * b*stride_b + h*stride_h + d. The launch grid depends only on batch,
- * num_kv_heads and max_context (which must be >= every context length);
- * rows with shorter contexts exit early, so a fixed max_context gives a
- * graph-capturable call. Page ids outside [0, num_blocks) read page 0
- * instead of faulting.
+ * b*stride_b + h*stride_h + d. The launch is persistent: its grid depends
+ * only on batch, num_kv_heads, max_context (which must be >= every context
+ * length) and the device, and the workgroups claim (sequence, partition,
+ * kv head) items from the workspace counters on the device, so a fixed
+ * max_context gives a graph-capturable call. batch <= 4096. Page ids
+ * outside [0, num_blocks) read page 0 instead of faulting.
  */
 int nimbus_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
                         const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,

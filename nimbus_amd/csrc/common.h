@@ -127,6 +127,21 @@ __device__ __forceinline__ f32x4 mfma_16x16x16<kBFloat16>(u32x2 a, u32x2 b, f32x
                                                    0, 0, 0);
 }
 
+// ---------------------------------------------------------------- transposed LDS reads
+
+// ds_read_b64_tr_b16 (gfx950). Within each 16-lane group, lane j supplies
+// the address of 4 consecutive 16-bit elements A_j[0..3]; lane i of the
+// group receives out[k] = A_{4k + i/4}[i % 4], k = 0..3. So if lane j of
+// group grp points at M[4 grp + j/4][c0 + 4 (j%4)] of a row-major 16-bit
+// matrix M, lane (i, grp) receives M[4 grp + k][c0 + i], k = 0..3: the
+// A operand of a 16x16x16 MFMA holding M^T (rows c0..c0+15, k = rows of M).
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4;
+  const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<uint16_t*>(p)));
+  return __builtin_bit_cast(u32x2, v);
+}
+
 // ---------------------------------------------------------------- wave reductions
 
 // Butterfly over the four 16-lane groups of a wave64 (lanes l, l^16, l^32, l^48).

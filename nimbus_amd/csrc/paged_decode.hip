@@ -3,38 +3,56 @@
 // Replaces nimbus/kernels/paged_attention.py:25-146 (the Triton
 // _paged_decode_kernel, _merge_partitions_kernel and their wrapper).
 //
-// Work split. The context of every sequence is cut into partitions of
-// PART tokens (page aligned). One workgroup of four waves owns one
-// (partition, kv head, sequence) and serves every query head that shares the
-// kv head, so each K/V page is read from HBM exactly once. Inside the
-// workgroup, wave w takes the 32-token chunks (two 16-token pages) w, w+4, ...
-// The launch grid is (ceil(max_context / PART), KV * ceil(G / 16), B): it depends
-// only on host integers, so a call is capturable in a hipGraph; partitions
-// past a sequence's end exit at once.
+// Work split (stream-K over the batch's pages). The 16-token pages of all
+// sequences are laid end to end. For each kv-head group (a kv head and up to
+// 16 of the query heads that share it, so each K/V page is read from HBM
+// once) the launch has the same number of waves, and wave i takes the i-th
+// equal slice of that page sequence. Every wave therefore streams the same
+// number of bytes (+-1 page) whatever the mix of context lengths; a slice
+// may end inside one sequence and continue into the next.
 //
-// Per chunk, with G query heads padded to 16 MFMA columns:
+// Each wave is its own workgroup (64 threads): no barriers, no atomics, no
+// state kept between calls. It first turns context_lens into the page
+// prefix sum in LDS, then walks its slice one page at a time. Decode is
+// bound by HBM latency as much as bandwidth, so each wave keeps kRing pages
+// of K/V in flight in a ring of register buffers (page x + kRing is issued
+// as soon as page x has been consumed), and finds each page's id kRing + 2
+// pages ahead with scalar loads that never wait behind the vector loads.
+// Per page, with G query heads padded to 16 MFMA columns:
 //   S^T[token][g] = K[token][:] . Q^T[:][g]   (16x16x32 MFMA, K straight from
 //                                               HBM into the A-operand layout)
 //   online softmax per column g in fp32 (exp2 domain), reductions across the
 //   four 16-lane groups with lane shuffles
-//   O^T[d][g]    += V^T[d][token] . P^T[token][g]  (16x16x16 fp16 MFMA; P^T
-//                                               is the QK output layout as is;
-//                                               V is converted to fp16 while
-//                                               staged through LDS, read
-//                                               transposed)
-// The four waves' partial (m, l, O) are merged through LDS. A sequence that
-// fits in one partition is normalised and written directly; otherwise the
-// partition writes fp32 (O, m, l) and paged_decode_merge_kernel combines
-// them (empty partitions never exist: a partition index below
-// ceil(ctx / PART) always holds at least one token).
+//   O^T[d][g]    += V^T[d][token] . P^T[token][g]  (16x16x16 MFMA; P^T is
+//                                               the QK output layout as is; V
+//                                               is staged through LDS as
+//                                               loaded and read back
+//                                               transposed with
+//                                               ds_read_b64_tr_b16)
+// For bf16 the PV product keeps V exact and carries P as two bf16 terms
+// (hi + lo, ~16 mantissa bits): rounding P to one bf16 alone costs ~8e-3
+// at |o| ~ 0.5, beyond the output tolerance. For fp16, P is one fp16.
+// When its slice covers a whole sequence the wave writes the normalised
+// output. Otherwise it writes fp32 (O, m, l) for its piece to slot
+// (wave + sequence), which no other wave uses, and paged_decode_merge_kernel
+// combines the pieces (the reference's _merge_partitions_kernel rule).
+//
+// The grid depends only on host integers (batch, kv heads, max_context and
+// the device's CU count), so a call is capturable in a hipGraph, and no
+// workgroup is launched beyond what the chip holds at once.
 #include "common.h"
 #include "nimbus_attn_internal.h"
 
 namespace nimbus {
 
-constexpr int kDecodeWaves = 4;
-constexpr int kDecodeThreads = 64 * kDecodeWaves;
-constexpr int kChunk = 32;  // tokens per wave iteration: two pages
+constexpr int kPage = 16;             // tokens per page (the only block size)
+constexpr int kMinPagesPerWave = 8;   // slices shorter than this only add merge work
+constexpr int kMaxDecodeBatch = 4096; // LDS holds the batch's page prefix sum
+constexpr int kWavesPerCU = 8;        // two waves of the page kernel per SIMD
+constexpr int kRing = 3;              // pages of K/V in flight per wave
+// gfx950 parts have 256 CUs; launches never exceed this many resident waves,
+// which keeps the workspace size a pure function of the call's shape.
+constexpr int64_t kMaxResidentWaves = 256 * kWavesPerCU;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -49,284 +67,418 @@ struct DecodeArgs {
   const int32_t* ctx;
   uint16_t* out;
   int64_t o_sb, o_sh;
-  float* part_o;   // [B, H, P, D]
-  float* part_ml;  // [B, H, P, 2]
-  int32_t H, G, gchunks, P;
+  int32_t* pre_out;  // workspace: the page prefix sum [B + 1], for the merge pass
+  float* part_ml;    // workspace: [slot][H][2] (m, l) of partial pieces
+  float* part_o;     // workspace: [slot][H][D] unnormalised O of partial pieces
+  int32_t B, H, G, gchunks, kvg;
+  int32_t nwk;       // waves launched per kv-head group
+  int32_t max_ctx;   // context bound: min(max_context, block-table width * 16)
   float scale_log2;
-};
-
-// LDS: per-wave staging of one chunk of V, later reused for the cross-wave merge.
-template <int D>
-struct DecodeSmem {
-  static constexpr int kVRow = D + 4;  // u16 stride; rows 4 apart land on different banks
-  static constexpr int kVBytes = kDecodeWaves * kChunk * kVRow * 2;
-  static constexpr int kMergeBytes = kDecodeWaves * (16 * D + 32) * 4;
-  static constexpr int kBytes = kVBytes > kMergeBytes ? kVBytes : kMergeBytes;
 };
 
 __device__ __forceinline__ int clamp_page(int32_t pid, int32_t nb) {
   return static_cast<uint32_t>(pid) < static_cast<uint32_t>(nb) ? pid : 0;
 }
 
-template <int DT, int D, int PART>
-__global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(DecodeArgs a) {
-  constexpr int KK = D / 32;              // 16x16x32 steps over the head dim
+__device__ __forceinline__ int pages_of(const DecodeArgs& a, int b) {
+  const int ctx = min(a.ctx[b], a.max_ctx);
+  return ctx > 0 ? (ctx + kPage - 1) / kPage : 0;
+}
+
+// p[i] for a wave-uniform i, read through the scalar cache: a load the
+// kernel never writes, which therefore does not wait behind vector loads.
+__device__ __forceinline__ int32_t scalar_load(const int32_t* p, int i) {
+  typedef const __attribute__((address_space(4))) int32_t* const_ptr;
+  return ((const_ptr)(p))[i];
+}
+
+// Waves per kv-head group that get a slice: all launched ones, unless the
+// batch is so short that slices would drop below kMinPagesPerWave pages.
+__device__ __forceinline__ int active_waves(int total_pages, int nwk) {
+  return max(1, min(nwk, total_pages / kMinPagesPerWave));
+}
+
+// First page of slice i out of nw over total pages.
+__device__ __forceinline__ int slice_start(int i, int nw, int total) {
+  return static_cast<int>(static_cast<int64_t>(i) * total / nw);
+}
+
+// The slice holding page x: the largest i with slice_start(i) <= x.
+__device__ __forceinline__ int slice_owner(int x, int nw, int total) {
+  return static_cast<int>((static_cast<int64_t>(x + 1) * nw - 1) / total);
+}
+
+// Exclusive prefix sum of per-sequence page counts into pre[0..B], by one wave.
+__device__ void page_prefix(const DecodeArgs& a, int* pre) {
+  const int lane = threadIdx.x;
+  const int per = (a.B + 63) / 64;
+  const int lo = min(lane * per, a.B);
+  const int hi = min(lo + per, a.B);
+  int s = 0;
+  for (int i = lo; i < hi; ++i) s += pages_of(a, i);
+  int incl = s;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off, 64);
+    if (lane >= off) incl += t;
+  }
+  int run = incl - s;
+  for (int i = lo; i < hi; ++i) {
+    pre[i] = run;
+    run += pages_of(a, i);
+  }
+  if (lo < hi && hi == a.B) pre[a.B] = run;
+  __syncthreads();
+}
+
+template <int D>
+struct PageBuf {
+  static constexpr int KK = D / 32;           // 16x16x32 steps over the head dim
+  static constexpr int VL = kPage * D / 512;  // 16-byte V loads per lane per page
+  u32x4 k[KK];                                // K in the QK A-operand layout
+  u32x4 v[VL];                                // V rows as loaded
+};
+
+// Where page p of sequence b lives (all wave-uniform). The loads are kept
+// raw: what depends on them is computed where it is used, so nothing waits
+// for them before it has to.
+struct PageRef {
+  int b, p, ctx_raw, pid_raw;
+};
+
+// Swizzled position of 16-byte chunk c of V row r in LDS: rows are read
+// sixteen at a time by the transposed PV operand loads, and spreading equal
+// chunks of different rows over different banks keeps those reads
+// conflict-free up to the LDS bandwidth.
+template <int D>
+__device__ __forceinline__ int v_pos(int r, int c) {
+  return c ^ ((2 * r) & (D / 8 - 1));
+}
+
+template <int DT, int D>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeArgs a) {
+  constexpr int KK = D / 32;
   constexpr int NN = D / 16;              // 16-row blocks of O^T
   constexpr int LPT = D / 8;              // lanes per token row (16 bytes each)
   constexpr int TPL = 64 / LPT;           // token rows per wave-wide load
-  constexpr int VLOADS = kChunk / TPL;    // 16-byte V loads per lane per chunk
-  constexpr int VROW = DecodeSmem<D>::kVRow;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[DecodeSmem<D>::kBytes];
+  constexpr int VL = PageBuf<D>::VL;
+  __shared__ __attribute__((aligned(16))) uint16_t vb[kPage * D];  // one page of V, rows swizzled
+  extern __shared__ int pre[];  // [B + 1]
 
-  const int part = blockIdx.x;
-  const int kvh = blockIdx.y / a.gchunks;
-  const int g0 = (blockIdx.y % a.gchunks) * 16;
-  const int b = blockIdx.z;
-
-  int ctx = a.ctx[b];
-  ctx = min(ctx, min(a.P * PART, a.bt_width * 16));
-  const int n_parts = (ctx + PART - 1) / PART;
-  if (part >= n_parts) return;
-
-  const int tok0 = part * PART;
-  const int tok1 = min(tok0 + PART, ctx);
-  const int n_pages = (tok1 - tok0 + 15) / 16;
-  const int n_chunks = (n_pages + 1) / 2;
-
-  const int tid = threadIdx.x;
-  const int wave = tid / 64;
-  const int lane = tid % 64;
+  const int lane = threadIdx.x;
   const int col = lane % 16;
   const int grp = lane / 16;
-  const int g = g0 + col;
-  const bool g_ok = g < a.G;
-  const int h = kvh * a.G + (g_ok ? g : 0);
+  const int kg = blockIdx.x % a.kvg;
+  const int idx = blockIdx.x / a.kvg;
+  const int kvh = kg / a.gchunks;
+  const int g0 = (kg % a.gchunks) * 16;
+  const bool g_ok = g0 + col < a.G;
+  const int head = kvh * a.G + (g_ok ? g0 + col : 0);
 
-  // Q^T as the B operand: column g, k-group grp holds q[g][32kk + 8grp .. +8].
-  u32x4 qop[KK];
-  {
-    const uint16_t* qrow = a.q + b * a.q_sb + static_cast<int64_t>(h) * a.q_sh;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      u32x4 v = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * grp);
-      qop[kk] = g_ok ? v : u32x4{0, 0, 0, 0};
-    }
+  page_prefix(a, pre);
+  const int total = __builtin_amdgcn_readfirstlane(pre[a.B]);
+  if (blockIdx.x == 0) {
+    for (int i = lane; i <= a.B; i += 64) a.pre_out[i] = pre[i];
   }
+  const int nw = active_waves(total, a.nwk);
+  if (idx >= nw || total == 0) return;
+  const int lo = slice_start(idx, nw, total);
+  const int hi = slice_start(idx + 1, nw, total);
+  if (lo >= hi) return;
 
-  const int32_t* btrow = a.bt + b * a.bt_sb + tok0 / 16;
   const uint16_t* kbase = a.kc + static_cast<int64_t>(kvh) * a.c_sh;
   const uint16_t* vbase = a.vc + static_cast<int64_t>(kvh) * a.c_sh;
-  uint16_t* vb = reinterpret_cast<uint16_t*>(smem) + wave * kChunk * VROW;
 
+  // Q^T as the B operand: column g, k-group grp holds q[g][32kk + 8grp .. +8].
+  // Columns past G read head kvh * G (a valid row) and are never written, so
+  // the load needs no mask and nothing waits for it before its first use.
+  auto load_q = [&](int b, u32x4* dst) {
+    const uint16_t* qrow = a.q + b * a.q_sb + static_cast<int64_t>(head) * a.q_sh;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) dst[kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * grp);
+  };
+
+  // First sequence of the slice: the largest b with pre[b] <= lo; `cursor`
+  // then only moves forward.
+  int cursor = 0;
+  {
+    int l = 0, h = a.B;
+    while (h - l > 1) {
+      const int mid = (l + h) >> 1;
+      if (pre[mid] <= lo) l = mid;
+      else h = mid;
+    }
+    cursor = l;
+  }
+  auto locate = [&](int y) {
+    PageRef r;
+    if (y < hi) {
+      while (pre[cursor + 1] <= y) ++cursor;
+      r.b = __builtin_amdgcn_readfirstlane(cursor);
+      r.p = __builtin_amdgcn_readfirstlane(y - pre[cursor]);
+      r.ctx_raw = scalar_load(a.ctx, r.b);
+      r.pid_raw = scalar_load(a.bt + r.b * a.bt_sb, r.p);
+    } else {
+      r.b = -1;
+      r.p = 0;
+      r.ctx_raw = 0;
+      r.pid_raw = 0;
+    }
+    return r;
+  };
+  auto load_page = [&](PageBuf<D>& bf, const PageRef& r) {
+    const int64_t off = static_cast<int64_t>(clamp_page(r.pid_raw, a.num_blocks)) * a.c_sb;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      bf.k[kk] = *reinterpret_cast<const u32x4*>(kbase + off + col * a.c_st + 32 * kk + 8 * grp);
+    }
+#pragma unroll
+    for (int r2 = 0; r2 < VL; ++r2) {
+      const int tt = r2 * TPL + lane / LPT;
+      bf.v[r2] = *reinterpret_cast<const u32x4*>(vbase + off + tt * a.c_st + 8 * (lane % LPT));
+    }
+  };
+
+  // ref[i] describes page x + i of the step about to run.
+  PageRef ref[kRing + 2];
+#pragma unroll
+  for (int i = 0; i < kRing + 2; ++i) ref[i] = locate(lo + i);
+  PageBuf<D> buf[kRing];
+#pragma unroll
+  for (int i = 0; i < kRing; ++i) {
+    if (lo + i < hi) load_page(buf[i], ref[i]);
+  }
+  u32x4 qop[KK], qnext[KK];
+  load_q(ref[0].b, qop);
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk) qnext[kk] = qop[kk];
+
+  // This lane's staging slots (row, swizzled chunk) and its transposed-read
+  // addresses: lane j of group grp reads row 4 grp + j/4, elements
+  // 16 nn + 4 (j%4) .. +4 (see lds_read_tr16).
+  uint16_t* stage[VL];
+#pragma unroll
+  for (int r2 = 0; r2 < VL; ++r2) {
+    const int tt = r2 * TPL + lane / LPT;
+    stage[r2] = vb + tt * D + 8 * v_pos<D>(tt, lane % LPT);
+  }
+  const int tr_row = 4 * grp + col / 4;
+  const uint16_t* tr_base = vb + tr_row * D + 4 * ((col % 4) % 2);
+  const int tr_chunk = (col % 4) / 2;
+
+  int seg0 = lo;  // first flat page of the current piece
   float m_run = -INFINITY;
   float l_run = 0.f;
   f32x4 acc[NN];
 #pragma unroll
   for (int nn = 0; nn < NN; ++nn) acc[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Registers of one chunk: K in A-operand layout, V rows as loaded.
-  u32x4 kreg[2][KK];
-  u32x4 vreg[VLOADS];
+  // One page: consume buffer bf (page x), refill it with page x + kRing.
+  auto step = [&](PageBuf<D>& bf, int x) {
+    const PageRef cur = ref[0];
+    const bool more = x + 1 < hi;
+    const bool piece_ends = !more || ref[1].b != cur.b;
+    ref[kRing + 1] = locate(x + kRing + 1);  // scalar loads, used two steps from now
+    const int valid = min(kPage, min(cur.ctx_raw, a.max_ctx) - kPage * cur.p);  // >= 1
 
-  auto load_chunk = [&](int c) {
-    const int p0 = 2 * c;
-    const bool has1 = p0 + 1 < n_pages;
-    const int pid0 = clamp_page(btrow[p0], a.num_blocks);
-    const int pid1 = has1 ? clamp_page(btrow[p0 + 1], a.num_blocks) : pid0;
-    const int64_t off0 = static_cast<int64_t>(pid0) * a.c_sb;
-    const int64_t off1 = static_cast<int64_t>(pid1) * a.c_sb;
+    // Stage V as loaded. Rows past the context (only on a sequence's last
+    // page) are zeroed: P is 0 there, but 0 * garbage must not reach the sum.
+    if (valid < kPage) {
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      kreg[0][kk] = *reinterpret_cast<const u32x4*>(kbase + off0 + col * a.c_st + 32 * kk + 8 * grp);
-    }
-    if (has1) {
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        kreg[1][kk] = *reinterpret_cast<const u32x4*>(kbase + off1 + col * a.c_st + 32 * kk + 8 * grp);
-      }
-    } else {
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) kreg[1][kk] = u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int tt = r * TPL + lane / LPT;
-      const int cc = lane % LPT;
-      const bool second = tt >= 16;
-      if (!second || has1) {
-        const int64_t off = second ? off1 : off0;
-        vreg[r] = *reinterpret_cast<const u32x4*>(vbase + off + (tt % 16) * a.c_st + 8 * cc);
-      } else {
-        vreg[r] = u32x4{0, 0, 0, 0};
+      for (int r2 = 0; r2 < VL; ++r2) {
+        if (r2 * TPL + lane / LPT >= valid) bf.v[r2] = u32x4{0, 0, 0, 0};
       }
     }
-  };
+#pragma unroll
+    for (int r2 = 0; r2 < VL; ++r2) *reinterpret_cast<u32x4*>(stage[r2]) = bf.v[r2];
 
-  int c = wave;
-  if (c < n_chunks) load_chunk(c);
-  for (; c < n_chunks; c += kDecodeWaves) {
-    // Stage V (zeroing rows past the context: 0 * garbage must not reach the sum).
-    const int valid = tok1 - (tok0 + kChunk * c);
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int tt = r * TPL + lane / LPT;
-      const int cc = lane % LPT;
-      u32x4 v = tt < valid ? vreg[r] : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = v_to_f16_pair<DT>(v[e]);
-      u32x2* dst = reinterpret_cast<u32x2*>(vb + tt * VROW + 8 * cc);
-      dst[0] = u32x2{v[0], v[1]};
-      dst[1] = u32x2{v[2], v[3]};
-    }
-    // S^T for both pages.
-    f32x4 s[2];
-#pragma unroll
-    for (int pi = 0; pi < 2; ++pi) {
-      f32x4 t = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) t = mfma_16x16x32<DT>(kreg[pi][kk], qop[kk], t);
-      s[pi] = t;
-    }
-    // Next chunk's loads go out before the softmax and PV of this one.
-    if (c + kDecodeWaves < n_chunks) load_chunk(c + kDecodeWaves);
+    for (int kk = 0; kk < KK; ++kk) s = mfma_16x16x32<DT>(bf.k[kk], qop[kk], s);
+
+    // Refill this buffer (and fetch the next sequence's Q) before the
+    // softmax and PV of this page.
+    if (x + kRing < hi) load_page(bf, ref[kRing]);
+    if (piece_ends && more) load_q(ref[1].b, qnext);
 
     float mx = -INFINITY;
 #pragma unroll
-    for (int pi = 0; pi < 2; ++pi) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = 16 * pi + 4 * grp + r;
-        const float x = t < valid ? s[pi][r] * a.scale_log2 : -INFINITY;
-        s[pi][r] = x;
-        mx = fmaxf(mx, x);
-      }
+    for (int r = 0; r < 4; ++r) {
+      const float xs = 4 * grp + r < valid ? s[r] * a.scale_log2 : -INFINITY;
+      s[r] = xs;
+      mx = fmaxf(mx, xs);
     }
     mx = max_across_groups(mx);
     const float m_new = fmaxf(m_run, mx);
     const float alpha = exp2f(m_run - m_new);
     m_run = m_new;
-    float psum = 0.f;
-    u32x2 pop[2];
+    float p[4];
 #pragma unroll
-    for (int pi = 0; pi < 2; ++pi) {
-      float p[4];
+    for (int r = 0; r < 4; ++r) p[r] = exp2f(s[r] - m_new);
+    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    // Once the running max settles it rarely moves: skip the rescale then.
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
+#pragma unroll
+      for (int nn = 0; nn < NN; ++nn) acc[nn] *= alpha;
+    }
+
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if constexpr (DT == kBFloat16) {
+      // V stays exact in bf16; P is carried as bf16 hi + lo (~16 bits).
+      uint16_t hi16[4], lo16[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        p[r] = exp2f(s[pi][r] - m_new);
-        psum += p[r];
+        hi16[r] = f32_to_bf16(p[r]);
+        lo16[r] = f32_to_bf16(p[r] - bf16_to_f32(hi16[r]));
       }
-      pop[pi] = u32x2{pack2(f32_to_f16(p[0]), f32_to_f16(p[1])), pack2(f32_to_f16(p[2]), f32_to_f16(p[3]))};
-    }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int nn = 0; nn < NN; ++nn) acc[nn] *= alpha;
-
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-    for (int pi = 0; pi < 2; ++pi) {
-      const uint16_t* vrow = vb + (16 * pi + 4 * grp) * VROW + col;
+      const u32x2 p_hi = u32x2{pack2(hi16[0], hi16[1]), pack2(hi16[2], hi16[3])};
+      const u32x2 p_lo = u32x2{pack2(lo16[0], lo16[1]), pack2(lo16[2], lo16[3])};
 #pragma unroll
       for (int nn = 0; nn < NN; ++nn) {
-        const uint16_t* p = vrow + 16 * nn;
-        u32x2 vop = u32x2{pack2(p[0], p[VROW]), pack2(p[2 * VROW], p[3 * VROW])};
-        acc[nn] = mfma_16x16x16<kFloat16>(vop, pop[pi], acc[nn]);
+        const u32x2 vop = lds_read_tr16(tr_base + 8 * v_pos<D>(tr_row, 2 * nn + tr_chunk));
+        acc[nn] = mfma_16x16x16<kBFloat16>(vop, p_hi, acc[nn]);
+        acc[nn] = mfma_16x16x16<kBFloat16>(vop, p_lo, acc[nn]);
+      }
+    } else {
+      const u32x2 pop = u32x2{pack2(f32_to_f16(p[0]), f32_to_f16(p[1])), pack2(f32_to_f16(p[2]), f32_to_f16(p[3]))};
+#pragma unroll
+      for (int nn = 0; nn < NN; ++nn) {
+        const u32x2 vop = lds_read_tr16(tr_base + 8 * v_pos<D>(tr_row, 2 * nn + tr_chunk));
+        acc[nn] = mfma_16x16x16<kFloat16>(vop, pop, acc[nn]);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
 
-  l_run = sum_across_groups(l_run);
-
-  // Cross-wave merge through LDS (reusing the V staging space).
-  __syncthreads();
-  float* mo = reinterpret_cast<float*>(smem);          // [wave][16][D]
-  float* mm = mo + kDecodeWaves * 16 * D;               // [wave][16]
-  float* ml = mm + kDecodeWaves * 16;                   // [wave][16]
+    if (piece_ends) {
+      // Finish the piece [seg0, x] of sequence cur.b.
+      const int rb = cur.b;
+      const float l = sum_across_groups(l_run);
+      const bool whole = seg0 == pre[rb] && x + 1 == pre[rb + 1];
+      if (g_ok) {
+        if (whole) {
+          const float inv = 1.f / l;
+          uint16_t* orow = a.out + rb * a.o_sb + static_cast<int64_t>(head) * a.o_sh;
 #pragma unroll
-  for (int nn = 0; nn < NN; ++nn) {
+          for (int nn = 0; nn < NN; ++nn) {
+            const f32x4 o = acc[nn];
+            const u32x2 w = u32x2{pack2(Elem<DT>::from_f32(o[0] * inv), Elem<DT>::from_f32(o[1] * inv)),
+                                  pack2(Elem<DT>::from_f32(o[2] * inv), Elem<DT>::from_f32(o[3] * inv))};
+            *reinterpret_cast<u32x2*>(orow + 16 * nn + 4 * grp) = w;
+          }
+        } else {
+          const int64_t row = (static_cast<int64_t>(idx) + rb) * a.H + head;
+          float* po = a.part_o + row * D;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) mo[(wave * 16 + col) * D + 16 * nn + 4 * grp + r] = acc[nn][r];
-  }
-  if (grp == 0) {
-    mm[wave * 16 + col] = m_run;
-    ml[wave * 16 + col] = l_run;
-  }
-  __syncthreads();
-
-  const int gcount = min(16, a.G - g0);
-  const bool single = n_parts == 1;
-  for (int idx = tid; idx < gcount * D; idx += kDecodeThreads) {
-    const int cg = idx / D;
-    const int d = idx % D;
-    float M = -INFINITY;
+          for (int nn = 0; nn < NN; ++nn) *reinterpret_cast<f32x4*>(po + 16 * nn + 4 * grp) = acc[nn];
+          if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run, l);
+        }
+      }
+      m_run = -INFINITY;
+      l_run = 0.f;
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) M = fmaxf(M, mm[w * 16 + cg]);
-    float L = 0.f, O = 0.f;
+      for (int nn = 0; nn < NN; ++nn) acc[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int w = 0; w < kDecodeWaves; ++w) {
-      const float wt = exp2f(mm[w * 16 + cg] - M);
-      L += ml[w * 16 + cg] * wt;
-      O += mo[(w * 16 + cg) * D + d] * wt;
+      for (int kk = 0; kk < KK; ++kk) qop[kk] = qnext[kk];
+      seg0 = x + 1;
     }
-    const int hh = kvh * a.G + g0 + cg;
-    if (single) {
-      a.out[b * a.o_sb + static_cast<int64_t>(hh) * a.o_sh + d] = Elem<DT>::from_f32(O / L);
-    } else {
-      const int64_t row = (static_cast<int64_t>(b) * a.H + hh) * a.P + part;
-      a.part_o[row * D + d] = O;
-      if (d == 0) {
-        a.part_ml[row * 2] = M;
-        a.part_ml[row * 2 + 1] = L;
+#pragma unroll
+    for (int i = 0; i < kRing + 1; ++i) ref[i] = ref[i + 1];
+  };
+
+  for (int x = lo; x < hi; x += kRing) {
+#pragma unroll
+    for (int k = 0; k < kRing; ++k) {
+      if (x + k >= hi) break;
+      step(buf[k], x + k);
+    }
+  }
+}
+
+// Second pass: for every sequence whose pages were split between waves,
+// o = sum_i O_i w_i / sum_i L_i w_i with w_i = 2^(m_i - max m) over its
+// pieces (nimbus/kernels/paged_attention.py:83-98), in one pass with a
+// running max. One wave per (sequence, kv-head group): lane = (head of the
+// group, 8 consecutive elements of d); sequences held whole by one wave exit
+// at once.
+template <int DT, int D>
+__global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
+  constexpr int SEG = D / 8;  // lanes per head
+  const int b = blockIdx.x;
+  const int kg = blockIdx.y;
+  const int total = a.pre_out[a.B];
+  const int first = a.pre_out[b];
+  const int last = a.pre_out[b + 1] - 1;
+  if (total == 0 || last < first) return;
+  const int nw = active_waves(total, a.nwk);
+  const int i0 = slice_owner(first, nw, total);
+  const int i1 = slice_owner(last, nw, total);
+  if (i0 == i1) return;
+  const int kvh = kg / a.gchunks;
+  const int g0 = (kg % a.gchunks) * 16;
+  const int gcount = min(16, a.G - g0);
+  for (int e = threadIdx.x; e < gcount * SEG; e += 64) {
+    const int head = kvh * a.G + g0 + e / SEG;
+    const int d0 = 8 * (e % SEG);
+    float M = -INFINITY, L = 0.f;
+    float O[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) O[k] = 0.f;
+    for (int i = i0; i <= i1; ++i) {
+      const int64_t row = (static_cast<int64_t>(i) + b) * a.H + head;
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+      const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
+      const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
+      const float Mn = fmaxf(M, ml.x);
+      const float wo = exp2f(M - Mn);
+      const float wi = exp2f(ml.x - Mn);
+      M = Mn;
+      L = L * wo + ml.y * wi;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        O[k] = O[k] * wo + o0[k] * wi;
+        O[k + 4] = O[k + 4] * wo + o1[k] * wi;
       }
     }
+    const float inv = 1.f / L;
+    uint16_t* orow = a.out + b * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
+    const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O[0] * inv), Elem<DT>::from_f32(O[1] * inv)),
+                          pack2(Elem<DT>::from_f32(O[2] * inv), Elem<DT>::from_f32(O[3] * inv)),
+                          pack2(Elem<DT>::from_f32(O[4] * inv), Elem<DT>::from_f32(O[5] * inv)),
+                          pack2(Elem<DT>::from_f32(O[6] * inv), Elem<DT>::from_f32(O[7] * inv))};
+    *reinterpret_cast<u32x4*>(orow) = w;
   }
 }
 
-// Second pass: combine a sequence's partitions, o = sum_p O_p w_p / sum_p L_p w_p
-// with w_p = 2^(m_p - max m). One wave per (head, sequence).
-template <int DT, int D, int PART>
-__global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
-  constexpr int DPL = D / 64;
-  const int hh = blockIdx.x;
-  const int b = blockIdx.y;
-  int ctx = a.ctx[b];
-  ctx = min(ctx, min(a.P * PART, a.bt_width * 16));
-  const int n = (ctx + PART - 1) / PART;
-  if (n <= 1) return;
-  const int64_t row0 = (static_cast<int64_t>(b) * a.H + hh) * a.P;
-  float M = -INFINITY;
-  for (int p = 0; p < n; ++p) M = fmaxf(M, a.part_ml[(row0 + p) * 2]);
-  float L = 0.f;
-  float O[DPL];
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) O[i] = 0.f;
-  const int lane = threadIdx.x;
-  for (int p = 0; p < n; ++p) {
-    const float wt = exp2f(a.part_ml[(row0 + p) * 2] - M);
-    L += a.part_ml[(row0 + p) * 2 + 1] * wt;
-#pragma unroll
-    for (int i = 0; i < DPL; ++i) O[i] += a.part_o[(row0 + p) * D + lane * DPL + i] * wt;
-  }
-  const float inv = 1.f / L;
-#pragma unroll
-  for (int i = 0; i < DPL; ++i) {
-    a.out[b * a.o_sb + static_cast<int64_t>(hh) * a.o_sh + lane * DPL + i] = Elem<DT>::from_f32(O[i] * inv);
-  }
+// Waves the launch gives each kv-head group: what the chip keeps resident,
+// capped by the pages the batch can hold (at least one).
+static int64_t waves_per_group(int64_t cus, int kvg, int64_t max_pages) {
+  const int64_t resident = cus * kWavesPerCU < kMaxResidentWaves ? cus * kWavesPerCU : kMaxResidentWaves;
+  int64_t n = resident / kvg;
+  if (n > max_pages / kMinPagesPerWave) n = max_pages / kMinPagesPerWave;
+  return n < 1 ? 1 : n;
 }
 
-// phase bit 1: partition pass, bit 2: merge pass.
-template <int DT, int D, int PART>
-static int launch_decode(const DecodeArgs& a, int batch, int kv_heads, int phases, hipStream_t stream) {
+static int device_cus(int64_t* cus) {
+  int dev = 0, n = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  *cus = n;
+  return static_cast<int>(e);
+}
+
+// phase bit 1: page pass, bit 2: merge pass.
+template <int DT, int D>
+static int launch_decode(const DecodeArgs& a, int phases, hipStream_t stream) {
   if (phases & 1) {
-    dim3 grid(a.P, kv_heads * a.gchunks, batch);
-    hipLaunchKernelGGL((paged_decode_kernel<DT, D, PART>), grid, dim3(kDecodeThreads), 0, stream, a);
+    const size_t dyn = static_cast<size_t>(a.B + 1) * sizeof(int);
+    hipLaunchKernelGGL((paged_decode_kernel<DT, D>), dim3(a.nwk * a.kvg), dim3(64), dyn, stream, a);
   }
-  if ((phases & 2) && a.P > 1) {
-    hipLaunchKernelGGL((paged_decode_merge_kernel<DT, D, PART>), dim3(a.H, batch), dim3(64), 0, stream, a);
+  if (phases & 2) {
+    hipLaunchKernelGGL((paged_decode_merge_kernel<DT, D>), dim3(a.B, a.kvg), dim3(64), 0, stream, a);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -335,39 +487,53 @@ static int launch_decode(const DecodeArgs& a, int batch, int kv_heads, int phase
 
 using namespace nimbus;
 
+// Workspace layout, each part 256-byte aligned: page prefix [B + 1] int32;
+// per slot (wave index + sequence, < waves per kv group + B) and query head
+// the (m, l) pair; per slot and head D floats of O.
+static int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
+static int64_t prefix_bytes(int64_t batch) { return round256((batch + 1) * 4); }
+
+static int64_t max_pages_of(int64_t batch, int64_t max_context) {
+  return batch * ((max_context + kPage - 1) / kPage);
+}
+
 extern "C" int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
                                                        int64_t max_context) {
   if (batch < 0 || num_heads <= 0 || head_dim <= 0 || max_context < 0) return -1;
-  const int64_t parts = (max_context + kDecodePartition - 1) / kDecodePartition;
-  if (parts <= 1) return 0;
-  return static_cast<int64_t>(batch) * num_heads * parts * (head_dim + 2) * 4;
+  // Any device and any kvg >= 1 launch at most this many waves per kv group.
+  const int64_t slots = waves_per_group(kMaxResidentWaves, 1, max_pages_of(batch, max_context)) + batch;
+  return prefix_bytes(batch) + round256(slots * num_heads * 2 * 4) + slots * num_heads * head_dim * 4;
 }
 
 static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
-                                   const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
-                                   int64_t cache_stride_token, int64_t cache_stride_head,
-                                   const int32_t* block_tables, int64_t bt_stride, int32_t bt_width,
-                                   const int32_t* context_lens, void* out, int64_t out_stride_b,
-                                   int64_t out_stride_h, void* workspace, int64_t workspace_bytes, int32_t batch,
-                                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                   int64_t max_context, float scale, int32_t dtype, void* stream) {
+                             const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                             int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                             int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
+                             int64_t out_stride_b, int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                             int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t block_size, int64_t max_context, float scale, int32_t dtype, void* stream) {
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return NIMBUS_ERR_INVALID;
-  if (block_size != 16) return NIMBUS_ERR_UNSUPPORTED;
+  if (block_size != kPage) return NIMBUS_ERR_UNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return NIMBUS_ERR_UNSUPPORTED;
   if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (batch > kMaxDecodeBatch || max_context > (int64_t{1} << 30)) return NIMBUS_ERR_UNSUPPORTED;
   if (batch == 0 || max_context <= 0) return NIMBUS_OK;
   if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out) return NIMBUS_ERR_INVALID;
   if (num_blocks <= 0 || num_blocks > INT32_MAX || bt_width <= 0) return NIMBUS_ERR_INVALID;
   // 16-byte vector access: 8-element aligned strides and bases.
-  if ((q_stride_b | q_stride_h | cache_stride_block | cache_stride_token | cache_stride_head) % 8 != 0)
+  if ((q_stride_b | q_stride_h | cache_stride_block | cache_stride_token | cache_stride_head | out_stride_b |
+       out_stride_h) % 8 != 0)
     return NIMBUS_ERR_ALIGNMENT;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
-       reinterpret_cast<uintptr_t>(v_cache)) % 16 != 0)
+       reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(out) |
+       reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
     return NIMBUS_ERR_ALIGNMENT;
   const int64_t need = nimbus_paged_decode_workspace_bytes(batch, num_heads, head_dim, max_context);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return NIMBUS_ERR_WORKSPACE;
-  const int64_t parts = (max_context + kDecodePartition - 1) / kDecodePartition;
-  if (parts > INT32_MAX / 16 || batch > 65535) return NIMBUS_ERR_UNSUPPORTED;
+  if (need < 0) return NIMBUS_ERR_INVALID;
+  if (workspace == nullptr || workspace_bytes < need) return NIMBUS_ERR_WORKSPACE;
+  int64_t cus = 0;
+  const int rc = device_cus(&cus);
+  if (rc != 0) return rc;
 
   DecodeArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -386,23 +552,31 @@ static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int6
   a.out = static_cast<uint16_t*>(out);
   a.o_sb = out_stride_b;
   a.o_sh = out_stride_h;
-  a.part_o = static_cast<float*>(workspace);
-  a.part_ml = need > 0 ? a.part_o + static_cast<int64_t>(batch) * num_heads * parts * head_dim : nullptr;
+  a.B = batch;
   a.H = num_heads;
   a.G = num_heads / num_kv_heads;
   a.gchunks = (a.G + 15) / 16;
-  a.P = static_cast<int32_t>(parts);
+  a.kvg = num_kv_heads * a.gchunks;
+  const int64_t ctx_bound = max_context < static_cast<int64_t>(bt_width) * kPage
+                                ? max_context
+                                : static_cast<int64_t>(bt_width) * kPage;
+  a.max_ctx = static_cast<int32_t>(ctx_bound);
+  // Never more waves per group than the workspace's slots were sized for.
+  const int64_t nwk = waves_per_group(cus, a.kvg, max_pages_of(batch, ctx_bound));
+  a.nwk = static_cast<int32_t>(nwk);
+  if (nwk * a.kvg > INT32_MAX / 2 || max_pages_of(batch, ctx_bound) > INT32_MAX / 2) return NIMBUS_ERR_UNSUPPORTED;
+  const int64_t slots = nwk + batch;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  a.pre_out = reinterpret_cast<int32_t*>(ws);
+  a.part_ml = reinterpret_cast<float*>(ws + prefix_bytes(batch));
+  a.part_o = reinterpret_cast<float*>(ws + prefix_bytes(batch) + round256(slots * num_heads * 2 * 4));
   a.scale_log2 = scale * 1.4426950408889634f;
-  if (num_kv_heads * a.gchunks > 65535) return NIMBUS_ERR_UNSUPPORTED;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
-  constexpr int P = kDecodePartition;
   if (dtype == kFloat16) {
-    return head_dim == 64 ? launch_decode<kFloat16, 64, P>(a, batch, num_kv_heads, phases, s)
-                          : launch_decode<kFloat16, 128, P>(a, batch, num_kv_heads, phases, s);
+    return head_dim == 64 ? launch_decode<kFloat16, 64>(a, phases, s) : launch_decode<kFloat16, 128>(a, phases, s);
   }
-  return head_dim == 64 ? launch_decode<kBFloat16, 64, P>(a, batch, num_kv_heads, phases, s)
-                        : launch_decode<kBFloat16, 128, P>(a, batch, num_kv_heads, phases, s);
+  return head_dim == 64 ? launch_decode<kBFloat16, 64>(a, phases, s) : launch_decode<kBFloat16, 128>(a, phases, s);
 }
 
 #define NIMBUS_DECODE_PARAMS                                                                                    \

@@ -22,6 +22,7 @@ import bisect
 
 import torch
 
+from nimbus_amd.kernels.paged_attention import decode_workspace_bytes, new_decode_workspace
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
 
 PADDED_SIZES = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128)
@@ -29,7 +30,7 @@ PADDED_SIZES = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128)
 
 class DecodeAttentionGraphs:
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, num_heads: int, scale: float,
-                 max_model_len: int, max_batch: int, scratch_block: int, backend: AttentionBackend | None = None):
+                 max_model_len: int, max_batch: int, scratch_block: int):
         self.k_cache, self.v_cache = k_cache, v_cache
         self.block_size = k_cache.shape[1]
         kv, d = k_cache.shape[2], k_cache.shape[3]
@@ -47,7 +48,9 @@ class DecodeAttentionGraphs:
         self.slots = torch.full((max_batch,), self.scratch_slot, dtype=torch.int64, device=dev)
         self.ctx = torch.ones(max_batch, dtype=torch.int32, device=dev)
         self.tables = torch.full((max_batch, width), scratch_block, dtype=torch.int32, device=dev)
-        self.backend = backend or AttentionBackend()
+        # The graphs' own decode workspace (item counters + split partials), zeroed once here.
+        self.workspace = new_decode_workspace(decode_workspace_bytes(max_batch, num_heads, d, max_model_len), dev)
+        self.backend = AttentionBackend(decode_workspace=self.workspace)
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata]] = {}
 
     def _meta(self, b: int) -> AttnMetadata:

@@ -24,6 +24,31 @@ def decode_workspace_bytes(batch: int, heads: int, head_dim: int, max_context: i
     return int(_lib.load().nimbus_paged_decode_workspace_bytes(batch, heads, head_dim, max_context))
 
 
+# Zero-initialised workspaces, one per (device, stream), grown on demand. A
+# call leaves the workspace's counter words at zero again, so a buffer is
+# zeroed once, when it is allocated. Buffers that were outgrown stay alive:
+# a captured graph may still read them.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+_OUTGROWN: list[torch.Tensor] = []
+
+
+def new_decode_workspace(nbytes: int, device) -> torch.Tensor:
+    """A workspace of at least nbytes that a decode call may use: zero-filled."""
+    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _cached_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _OUTGROWN.append(ws)
+        ws = new_decode_workspace(max(nbytes, 1 << 20), device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
         raise ValueError("k_cache and v_cache must both be [num_blocks, block_size, KV, D]")
@@ -60,9 +85,11 @@ def paged_decode_attention(
     the split is always PARTITION tokens, so the value is not used.
     `out` (optional, not in the reference signature) receives the result in
     place, e.g. a slice of the backend's flat output. `workspace` (optional)
-    is a caller-owned uint8 buffer of at least decode_workspace_bytes() for the
-    split-context partials; by default one is taken from torch's allocator per
-    call. `_entry` selects one
+    is a caller-owned uint8 buffer of at least decode_workspace_bytes(): the
+    work-item counters (zero when the buffer is first used, left zero by every
+    call; new_decode_workspace() makes one) and the split-context partials.
+    By default a cached zeroed workspace per (device, stream) is used, so
+    concurrent calls must run on different streams. `_entry` selects one
     pass of the C ABI (nimbus_paged_decode_partitions / _merge) for timing
     the passes separately; the default runs both.
     """
@@ -98,12 +125,12 @@ def paged_decode_attention(
             raise ValueError(f"workspace smaller than the {need} bytes this call needs")
         ws = workspace
     else:
-        ws = torch.empty(max(need, 0), dtype=torch.uint8, device=q.device) if need > 0 else None
+        ws = _cached_workspace(need, q.device)
     rc = getattr(lib, _entry)(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
         k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(), block_tables.stride(0),
         block_tables.shape[1], context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
-        _lib.ptr(ws), 0 if ws is None else ws.numel() * ws.element_size(), b, h, kv, d, k_cache.shape[1], int(max_context), float(scale),
+        ws.data_ptr(), ws.numel() * ws.element_size(), b, h, kv, d, k_cache.shape[1], int(max_context), float(scale),
         _lib.dtype_code(q.dtype), _lib.stream_of(q))
     _lib.check(rc, _entry)
     return out

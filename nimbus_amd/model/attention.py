@@ -61,11 +61,16 @@ class AttentionBackend:
     rejected rather than silently served by a CPU implementation.
     """
 
-    def __init__(self, use_hip: bool = True):
+    def __init__(self, use_hip: bool = True, decode_workspace: torch.Tensor | None = None):
+        """decode_workspace (not in the reference): a zeroed decode workspace
+        (item counters + split partials, see paged_decode_attention) for this
+        backend's decode calls instead of the per-stream cached one; a graph
+        capture passes its own, sized for its largest batch."""
         if not use_hip:
             raise ValueError("nimbus_amd's AttentionBackend is the HIP path only; use Nimbus's reference "
                              "backend for CPU execution")
         self.use_hip = True
+        self.decode_workspace = decode_workspace
         self._decode = paged_attention.paged_decode_attention
         self._prefill = prefill_attention.paged_prefill_attention
         self._build_programs = prefill_attention.build_programs
@@ -98,5 +103,6 @@ class AttentionBackend:
             self._decode(
                 q[p:], k_cache, v_cache, meta.decode_context_lens, meta.decode_block_tables,
                 meta.max_decode_context, scale, num_partitions=meta.decode_partitions, out=out[p:],
+                workspace=self.decode_workspace,
             )
         return out

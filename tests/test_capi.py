@@ -55,9 +55,18 @@ def test_one_hip_runtime_in_process():
 def test_workspace_bytes_is_a_pure_size_formula():
     lib = _lib.load()
     f = lib.nimbus_paged_decode_workspace_bytes
-    assert f(64, 32, 128, 512) == 0  # one partition: no partials
-    assert f(64, 32, 128, 513) == 64 * 32 * 2 * (128 + 2) * 4
-    assert f(64, 32, 128, 8192) == 64 * 32 * 16 * (128 + 2) * 4
+
+    def r256(n):
+        return -(-n // 256) * 256
+
+    def want(b, h, d, maxc):
+        waves = max(1, min(256 * 8, b * -(-maxc // 16) // 8))  # slices of >= 8 pages, <= resident waves
+        slots = waves + b  # one per (wave, sequence) piece
+        return r256((b + 1) * 4) + r256(slots * h * 2 * 4) + slots * h * d * 4  # prefix, (m, l), O
+
+    assert f(64, 32, 128, 8192) == want(64, 32, 128, 8192) == 512 + 2112 * 32 * 8 + 2112 * 32 * 512
+    assert f(1, 32, 128, 100) == want(1, 32, 128, 100) == 256 + 512 + 2 * 32 * 512
+    assert f(16, 32, 64, 1024) == want(16, 32, 64, 1024)
     assert f(-1, 32, 128, 8192) == -1
 
 
@@ -81,6 +90,8 @@ def _decode(**kw):
     (dict(qsh=100), _lib.NIMBUS_ERR_ALIGNMENT),
     (dict(q=DUMMY + 2), _lib.NIMBUS_ERR_ALIGNMENT),
     (dict(maxc=4096), _lib.NIMBUS_ERR_WORKSPACE),
+    (dict(maxc=64), _lib.NIMBUS_ERR_WORKSPACE),  # the chunk prefix is always needed
+    (dict(b=4097), _lib.NIMBUS_ERR_UNSUPPORTED),
     (dict(b=0), 0),
     (dict(maxc=0), 0),
 ])

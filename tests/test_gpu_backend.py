@@ -53,8 +53,13 @@ def test_mixed_step_matches_oracle():
 @pytest.mark.parametrize("n", [60, 3, 1])
 def test_decode_graph_replay_matches_eager(n):
     """Decode attention captured at padded sizes (padding rows on a scratch
-    block) equals the eager call on the real rows; every replay, with eager
-    work and synchronisations between replays, gives the same result."""
+    block): every replay, with eager work and synchronisations between
+    replays, is bit-identical to the eager call on the same padded inputs,
+    and the real rows agree with the eager call on the unpadded batch and
+    with the oracle within the output tolerance. (The decode kernel splits
+    the batch's chunks evenly over its waves, so padding rows move the split
+    points and change the fp32 summation order of the real rows: bitwise
+    equality holds only for identical inputs.)"""
     announce(f"graph replay n={n}")
     ctx = workloads.llama3_decode_lens(seed=n, batch=n)
     b = workloads.build_batch([(c, 1) for c in ctx], heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16,
@@ -81,10 +86,20 @@ def test_decode_graph_replay_matches_eager(n):
         decode_context_lens=da[3], decode_block_tables=da[4], max_decode_context=da[5],
         prefill_query_start_host=[0], prefill_context_lens_host=[])
     eager = AttentionBackend().forward(da[0], k_new, v_new, kc_e, vc_e, eager_meta, b.scale)
+    replays = []
     for rep in range(3):
-        got = graphs.run(da[0], k_new, v_new, slots, da[3], da[4]).clone()
+        replays.append(graphs.run(da[0], k_new, v_new, slots, da[3], da[4]).clone())
         torch.cuda.synchronize()
-        assert torch.equal(got, eager), f"replay {rep}"
         _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # eager work between replays
+    bp = graphs.padded_size(n)
+    padded_meta = graphs.graphs[bp][2]
+    kc_p, vc_p = kc.clone(), vc.clone()
+    padded = AttentionBackend().forward(graphs.q[:bp], graphs.k[:bp], graphs.v[:bp], kc_p, vc_p, padded_meta,
+                                        b.scale)[:n]
+    for rep, got in enumerate(replays):
+        assert torch.equal(got, padded), f"replay {rep} differs from eager on the padded batch"
+        assert_within(got.cpu(), eager.cpu().double(), what=f"replay {rep} vs eager")
     assert torch.equal(kc[:nb], kc_e[:nb]) and torch.equal(vc[:nb], vc_e[:nb])
-    assert_within(eager.cpu(), oracle_decode(da[0], kc_e, vc_e, ctx, da[4], b.scale), what="eager vs oracle")
+    want = oracle_decode(da[0], kc_e, vc_e, ctx, da[4], b.scale)
+    assert_within(eager.cpu(), want, what="eager vs oracle")
+    assert_within(replays[0].cpu(), want, what="replay vs oracle")
