@@ -11,9 +11,12 @@ A step is one paged_decode_attention call on inputs already resident in HBM.
 value        algorithmic bytes of one call / wall time per step (GB/s):
              every visible K and V row once, q and out once, the page ids and
              context lengths (nimbus_amd.workloads.decode_bytes)
-roofline     the partition pass (the dominant kernel) alone, timed with HIP
-             events on the launch stream: algorithmic bytes / its mean
-             duration, against 8 TB/s
+roofline     the page pass (paged_decode_kernel, the dominant kernel) alone,
+             timed with HIP events on the launch stream: algorithmic bytes /
+             its mean duration, against 8 TB/s; `traffic` is the HBM bytes
+             per launch that rocprofv3 FETCH_SIZE + WRITE_SIZE measured for
+             this kernel and workload (profiles/decode_llama3_traffic.json,
+             scaled by the plain-copy calibration), null when absent
 cpu_baseline the CPU oracle (restated nimbus/kernels/reference.py:71-96,
              batched exact form) on this host's cores, same inputs
 prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
@@ -78,6 +81,21 @@ def copy_calibration(mib):
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def measured_traffic(kernel, algorithmic_bytes):
+    """HBM bytes per launch of `kernel` on this workload as rocprofv3 counted
+    them (FETCH_SIZE + WRITE_SIZE, calibrated), from the committed profile
+    summary; None when there is none for this kernel and byte count."""
+    path = os.path.join(ROOT, "profiles", "decode_llama3_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if rec.get("kernel") != kernel or rec.get("algorithmic_bytes") != algorithmic_bytes:
+        return None
+    return rec.get("traffic_bytes")
 
 
 # ---------------------------------------------------------------- timing helpers
@@ -146,7 +164,7 @@ def time_decode(batch, steps, warmup, wall=True):
         torch.cuda.synchronize()
         res["ms_per_step"] = (time.perf_counter() - w0) * 1e3 / steps
     res["call_us"] = statistics.mean(event_times_us(call, steps, stream))
-    res["partition_us"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_partitions"),
+    res["page_pass_us"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_pages"),
                                                          steps, stream))
     res["merge_us"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_merge"), steps, stream))
     res["bytes"] = workloads.decode_bytes(ctx_lens, h, kv, d, batch.q.element_size())
@@ -279,8 +297,8 @@ def all_configs(steps, warmup):
         b = workloads.CONFIGS[name]("cuda")
         r = time_decode(b, steps, warmup, wall=False)
         r["GBps_call"] = r["bytes"] / r["call_us"] / 1e3
-        r["GBps_partition_pass"] = r["bytes"] / r["partition_us"] / 1e3
-        r["frac_hbm_peak_partition_pass"] = r["GBps_partition_pass"] / HBM_PEAK_GBS
+        r["GBps_page_pass"] = r["bytes"] / r["page_pass_us"] / 1e3
+        r["frac_hbm_peak_page_pass"] = r["GBps_page_pass"] / HBM_PEAK_GBS
         rows[name] = r
         del b
         torch.cuda.empty_cache()
@@ -327,7 +345,7 @@ def main(argv=None):
     batch = workloads.llama3_decode("cuda")
     dec = time_decode(batch, args.steps, args.warmup)
     log(f"decode: {dec}")
-    part_gbs = dec["bytes"] / dec["partition_us"] / 1e3
+    part_gbs = dec["bytes"] / dec["page_pass_us"] / 1e3
     result = {
         "metric": METRIC,
         "value": dec["bytes"] / (dec["ms_per_step"] * 1e-3) / 1e9,
@@ -349,14 +367,14 @@ def main(argv=None):
         },
         "us_per_call": dec["call_us"],
         "roofline": {
-            "kernel": "paged_decode_kernel (partition pass)",
+            "kernel": "paged_decode_kernel (page pass)",
             "bound": "hbm",
             "achieved": part_gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": part_gbs / HBM_PEAK_GBS,
-            "traffic": None,
-            "kernel_us": dec["partition_us"],
+            "traffic": measured_traffic("paged_decode_kernel", dec["bytes"]),
+            "kernel_us": dec["page_pass_us"],
             "merge_pass_us": dec["merge_us"],
         },
     }

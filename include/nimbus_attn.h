@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 1
+#define NIMBUS_ATTN_ABI_VERSION 2
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -64,18 +64,12 @@ int nimbus_write_kv(const void* k, const void* v, void* k_cache, void* v_cache, 
 
 /*
  * Bytes of workspace nimbus_paged_decode needs at this batch, head count,
- * head dim and max_context: NIMBUS_DECODE_COUNTER_BYTES of work-item
- * counters, then (when max_context spans more than one partition of
- * NIMBUS_DECODE_PARTITION tokens) fp32 split-context partial results.
- * Pure function of its arguments.
- *
- * The counter bytes must be zero before a workspace's first use; every
- * completed call leaves them zero again, so a caller zero-fills a workspace
- * once, when allocating it. Calls that run concurrently (on different
- * streams) need different workspaces.
+ * head dim and max_context (a pure function of its arguments): the batch's
+ * page prefix sum and room for fp32 (O, m, l) pieces of sequences whose
+ * pages are split between waves. The workspace carries nothing from one call
+ * to the next and needs no initialisation; calls that run concurrently (on
+ * different streams) need different workspaces.
  */
-#define NIMBUS_DECODE_COUNTER_BYTES 256
-#define NIMBUS_DECODE_PARTITION 512
 int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
                                             int64_t max_context);
 
@@ -87,12 +81,13 @@ int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, in
  * out[b, h, :] = softmax(scale * q[b, h] . K_b^T) V_b over the first
  * context_lens[b] tokens of sequence b, read through block_tables[b] from
  * kv head h / (num_heads / num_kv_heads). q/out: element (b, h, d) at
- * b*stride_b + h*stride_h + d. The launch is persistent: its grid depends
- * only on batch, num_kv_heads, max_context (which must be >= every context
- * length) and the device, and the workgroups claim (sequence, partition,
- * kv head) items from the workspace counters on the device, so a fixed
- * max_context gives a graph-capturable call. batch <= 4096. Page ids
- * outside [0, num_blocks) read page 0 instead of faulting.
+ * b*stride_b + h*stride_h + d. The batch's 16-token pages are split evenly
+ * over a fixed number of waves per kv-head group (a split may fall inside a
+ * sequence; a second pass merges such sequences' pieces). The launch grid
+ * depends only on batch, num_kv_heads, max_context (which must be >= every
+ * context length; longer contexts are cut to it) and the device's CU count,
+ * so a fixed max_context gives a graph-capturable call. batch <= 4096. Page
+ * ids outside [0, num_blocks) read page 0 instead of faulting.
  */
 int nimbus_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
                         const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
@@ -104,22 +99,20 @@ int nimbus_paged_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h, c
 
 /*
  * The two passes of nimbus_paged_decode, launchable on their own (same
- * arguments). nimbus_paged_decode_partitions replaces _paged_decode_kernel
- * (paged_attention.py:25-80): it writes the final output of every sequence
- * that fits in one partition and fp32 partials for the others.
- * nimbus_paged_decode_merge replaces _merge_partitions_kernel
- * (paged_attention.py:83-98): it combines those partials into the output
- * (nothing to do, and no launch, when max_context fits in one partition).
- * Running partitions then merge on one stream equals nimbus_paged_decode.
+ * arguments). nimbus_paged_decode_pages (the work of _paged_decode_kernel,
+ * paged_attention.py:25-80) writes the output of every sequence one wave
+ * held whole and fp32 pieces of the others; nimbus_paged_decode_merge (the
+ * work of _merge_partitions_kernel, paged_attention.py:83-98) combines those
+ * pieces into the output. Running pages then merge on one stream equals
+ * nimbus_paged_decode.
  */
-int nimbus_paged_decode_partitions(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
-                                   const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
-                                   int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
-                                   int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
-                                   int64_t out_stride_b, int64_t out_stride_h, void* workspace,
-                                   int64_t workspace_bytes, int32_t batch, int32_t num_heads, int32_t num_kv_heads,
-                                   int32_t head_dim, int32_t block_size, int64_t max_context, float scale,
-                                   int32_t dtype, void* stream);
+int nimbus_paged_decode_pages(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                              const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                              int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                              int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
+                              int64_t out_stride_b, int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                              int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t block_size, int64_t max_context, float scale, int32_t dtype, void* stream);
 int nimbus_paged_decode_merge(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
                               const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
                               int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,

@@ -52,13 +52,15 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
   return x;
 }
 
-// The P.V product of both attention kernels runs in fp16 whatever the cache
-// dtype: P lies in [0, 1], where fp16 keeps 3 more mantissa bits than bf16
+// The prefill kernel's P.V product runs in fp16 whatever the cache dtype:
+// P lies in [0, 1], where fp16 keeps 3 more mantissa bits than bf16
 // (rounding P to bf16 alone costs ~8e-3 at |o| ~ 0.5, beyond the output
 // tolerance), and a bf16 V element converts to fp16 exactly when
 // |v| <= 65504 (smaller magnitudes lose at most 2^-25 in fp16's subnormal
 // range). Larger |v| saturate to +-65504 rather than becoming inf, so one
 // outlier cannot turn masked-out products (0 * inf) into NaN for other rows.
+// (Decode, which cannot afford a per-element conversion of V, keeps V in
+// bf16 and splits P into two bf16 terms instead.)
 template <int DT>
 __device__ __forceinline__ uint16_t v_to_f16_bits(uint16_t x);
 

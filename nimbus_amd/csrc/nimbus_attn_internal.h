@@ -5,7 +5,6 @@
 
 namespace nimbus {
 
-constexpr int kDecodePartition = NIMBUS_DECODE_PARTITION;  // tokens per split-context partition
 constexpr int kPrefillTile = NIMBUS_PREFILL_TILE;          // query positions per tile-table entry
 
 }  // namespace nimbus

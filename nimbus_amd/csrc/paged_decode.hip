@@ -594,7 +594,7 @@ static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int6
 
 extern "C" int nimbus_paged_decode(NIMBUS_DECODE_PARAMS) { return paged_decode_impl(3, NIMBUS_DECODE_ARGS); }
 
-extern "C" int nimbus_paged_decode_partitions(NIMBUS_DECODE_PARAMS) {
+extern "C" int nimbus_paged_decode_pages(NIMBUS_DECODE_PARAMS) {
   return paged_decode_impl(1, NIMBUS_DECODE_ARGS);
 }
 

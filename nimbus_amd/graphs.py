@@ -48,7 +48,7 @@ class DecodeAttentionGraphs:
         self.slots = torch.full((max_batch,), self.scratch_slot, dtype=torch.int64, device=dev)
         self.ctx = torch.ones(max_batch, dtype=torch.int32, device=dev)
         self.tables = torch.full((max_batch, width), scratch_block, dtype=torch.int32, device=dev)
-        # The graphs' own decode workspace (item counters + split partials), zeroed once here.
+        # The graphs' own decode workspace (page prefix + split pieces), sized for the largest batch.
         self.workspace = new_decode_workspace(decode_workspace_bytes(max_batch, num_heads, d, max_model_len), dev)
         self.backend = AttentionBackend(decode_workspace=self.workspace)
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata]] = {}

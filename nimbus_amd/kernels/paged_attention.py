@@ -4,11 +4,13 @@ Drop-in for nimbus/kernels/paged_attention.py:101-146: same signature, same
 result (within fp16/bf16 rounding of the reference attention), computed by
 paged_decode_kernel + paged_decode_merge_kernel in csrc/paged_decode.hip.
 
-Context is split into PARTITION-token partitions for every sequence, so long
-contexts spread over many workgroups whatever the batch size. The launch grid
-is a function of (batch, KV heads, max_context) only; inside a captured graph
-the caller fixes max_context (Nimbus's DecodeGraphs passes max_model_len,
-cuda_graph.py:52-63) and the same graph serves any context lengths up to it.
+The batch's 16-token pages are split evenly over a fixed number of waves per
+kv-head group, so the work is balanced whatever the mix of context lengths
+and long contexts spread over many waves at any batch size. The launch grid
+is a function of (batch, KV heads, max_context, device) only; inside a
+captured graph the caller fixes max_context (Nimbus's DecodeGraphs passes
+max_model_len, cuda_graph.py:52-63) and the same graph serves any context
+lengths up to it.
 """
 
 from __future__ import annotations
@@ -17,24 +19,23 @@ import torch
 
 from nimbus_amd import _lib
 
-PARTITION = 512  # tokens per split-context partition (NIMBUS_DECODE_PARTITION)
+PAGE = 16  # tokens per KV-cache block: the only block size the kernels take
 
 
 def decode_workspace_bytes(batch: int, heads: int, head_dim: int, max_context: int) -> int:
     return int(_lib.load().nimbus_paged_decode_workspace_bytes(batch, heads, head_dim, max_context))
 
 
-# Zero-initialised workspaces, one per (device, stream), grown on demand. A
-# call leaves the workspace's counter words at zero again, so a buffer is
-# zeroed once, when it is allocated. Buffers that were outgrown stay alive:
-# a captured graph may still read them.
+# Workspaces cached per (device, stream), grown on demand, so a call does not
+# allocate. Buffers that were outgrown stay alive: a captured graph may still
+# use them.
 _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 _OUTGROWN: list[torch.Tensor] = []
 
 
 def new_decode_workspace(nbytes: int, device) -> torch.Tensor:
-    """A workspace of at least nbytes that a decode call may use: zero-filled."""
-    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+    """A workspace of at least nbytes for decode calls (no initialisation needed)."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
 def _cached_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
@@ -81,16 +82,15 @@ def paged_decode_attention(
     max_context must be >= every context length (the reference relies on the
     same bound for its grid and gather width). num_partitions is accepted for
     signature compatibility with the Triton wrapper, whose graph capture uses
-    it to pin the grid; here the grid is already pinned by max_context, and
-    the split is always PARTITION tokens, so the value is not used.
+    it to pin the grid; here the grid is already pinned by max_context, so
+    the value is not used.
     `out` (optional, not in the reference signature) receives the result in
     place, e.g. a slice of the backend's flat output. `workspace` (optional)
-    is a caller-owned uint8 buffer of at least decode_workspace_bytes(): the
-    work-item counters (zero when the buffer is first used, left zero by every
-    call; new_decode_workspace() makes one) and the split-context partials.
-    By default a cached zeroed workspace per (device, stream) is used, so
+    is a caller-owned uint8 buffer of at least decode_workspace_bytes() (the
+    page prefix sum and the pieces of split sequences; nothing in it survives
+    the call). By default a workspace cached per (device, stream) is used, so
     concurrent calls must run on different streams. `_entry` selects one
-    pass of the C ABI (nimbus_paged_decode_partitions / _merge) for timing
+    pass of the C ABI (nimbus_paged_decode_pages / _merge) for timing
     the passes separately; the default runs both.
     """
     del num_partitions

@@ -13,7 +13,7 @@ import pytest
 import torch
 
 from nimbus_amd import workloads
-from nimbus_amd.kernels.paged_attention import PARTITION, paged_decode_attention
+from nimbus_amd.kernels.paged_attention import PAGE, paged_decode_attention
 from oracle import closed_form
 from tests import golden_io
 from tests.gpu_helpers import announce, oracle_decode
@@ -75,9 +75,9 @@ def test_grid_width_does_not_change_results():
     assert torch.equal(a, b)
 
 
-def test_partition_boundaries_match_oracle():
-    announce("decode partition boundaries")
-    ctx_lens = [PARTITION - 1, PARTITION, PARTITION + 1, 2 * PARTITION, 2 * PARTITION + 16, 3 * PARTITION + 31]
+def test_page_boundaries_match_oracle():
+    announce("decode page boundaries")
+    ctx_lens = [PAGE - 1, PAGE, PAGE + 1, 2 * PAGE, 511, 512, 513, 1024 + PAGE, 1536 + 31]
     q, k, v, ctx, bt, scale = _case(32, 8, 128, ctx_lens, torch.bfloat16, seed=6)
     got = paged_decode_attention(q, k, v, ctx, bt, max(ctx_lens), scale)
     assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale), what="vs oracle")
