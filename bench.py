@@ -234,7 +234,7 @@ def time_prefill(batch, steps, warmup):
     from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
 
     args = batch.prefill_args()
-    progs = build_programs(args[7], batch.q.device)
+    progs = build_programs(args[7], batch.q.device, args[8])
     out = torch.empty_like(args[0])
 
     def call(i):
@@ -264,7 +264,7 @@ def time_mixed_step(batch, steps, warmup):
                                    max_batch=64, scratch_block=nb)
     graphs.capture()
     pa = batch.prefill_args()
-    progs = build_programs(pa[7], batch.q.device)
+    progs = build_programs(pa[7], batch.q.device, pa[8])
     p_tok = batch.num_prefill_tokens
     da = batch.decode_args()
     out = torch.empty_like(batch.q)

@@ -76,11 +76,23 @@ __device__ __forceinline__ uint16_t v_to_f16_bits<kBFloat16>(uint16_t x) {
   return f32_to_f16(f);
 }
 
-// Two 16-bit V elements packed in a dword, converted together.
+// Two 16-bit V elements packed in a dword, converted together: each half to
+// fp32 (a shift or a mask), clamped to the fp16 range with one med3, then
+// both packed by one v_cvt_pkrtz (exact for bf16 values in range, so the
+// conversion's rounding mode does not matter).
 template <int DT>
-__device__ __forceinline__ uint32_t v_to_f16_pair(uint32_t w) {
-  return static_cast<uint32_t>(v_to_f16_bits<DT>(static_cast<uint16_t>(w & 0xffffu))) |
-         (static_cast<uint32_t>(v_to_f16_bits<DT>(static_cast<uint16_t>(w >> 16))) << 16);
+__device__ __forceinline__ uint32_t v_to_f16_pair(uint32_t w);
+
+template <>
+__device__ __forceinline__ uint32_t v_to_f16_pair<kFloat16>(uint32_t w) {
+  return w;
+}
+
+template <>
+__device__ __forceinline__ uint32_t v_to_f16_pair<kBFloat16>(uint32_t w) {
+  const float lo = __builtin_amdgcn_fmed3f(__uint_as_float(w << 16), -65504.f, 65504.f);
+  const float hi = __builtin_amdgcn_fmed3f(__uint_as_float(w & 0xffff0000u), -65504.f, 65504.f);
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
 
 template <int DT> struct Elem;
@@ -143,6 +155,10 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
   const s16x4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(const_cast<uint16_t*>(p)));
   return __builtin_bit_cast(u32x2, v);
 }
+
+// 2^x with the bare v_exp_f32 (no denormal range reduction): softmax weights
+// below 2^-126 may flush to zero.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // ---------------------------------------------------------------- wave reductions
 

@@ -310,11 +310,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     }
     mx = max_across_groups(mx);
     const float m_new = fmaxf(m_run, mx);
-    const float alpha = exp2f(m_run - m_new);
+    const float alpha = fast_exp2(m_run - m_new);
     m_run = m_new;
     float p[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = exp2f(s[r] - m_new);
+    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(s[r] - m_new);
     l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
     // Once the running max settles it rarely moves: skip the rescale then.
     if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
@@ -433,8 +433,8 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
       const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
       const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
       const float Mn = fmaxf(M, ml.x);
-      const float wo = exp2f(M - Mn);
-      const float wi = exp2f(ml.x - Mn);
+      const float wo = fast_exp2(M - Mn);
+      const float wi = fast_exp2(ml.x - Mn);
       M = Mn;
       L = L * wo + ml.y * wi;
 #pragma unroll

@@ -19,20 +19,35 @@ from nimbus_amd.kernels.paged_attention import _check_cache
 BLOCK_M = 64  # query positions per tile-table entry (NIMBUS_PREFILL_TILE)
 
 
-def build_programs(query_start_host: list[int], device) -> tuple[torch.Tensor, torch.Tensor]:
+def build_programs(query_start_host: list[int], device,
+                   context_lens_host: list[int] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """(sequence index, first query offset) for every BLOCK_M query tile.
 
-    Same table as nimbus/kernels/prefill_attention.py:81-90, built with NumPy
-    instead of a Python loop and moved to the device in one copy. Nimbus's
-    backend builds it once per step and reuses it in every layer
+    Without context_lens_host this is the table of
+    nimbus/kernels/prefill_attention.py:81-90, in the same order, built with
+    NumPy instead of a Python loop and moved to the device in one copy.
+    Nimbus's backend builds it once per step and reuses it in every layer
     (model/attention.py:82-83).
+
+    With context_lens_host (not in the reference signature; the backend
+    passes it) the same entries are ordered for the MI355X launch: by cost
+    (the keys the tile's last query sees), heaviest first, and the lighter
+    half reversed, so that workgroups launched half a grid apart, which
+    share a CU, pair a heavy tile with a light one.
     """
     qs = np.asarray(query_start_host, dtype=np.int64)
     lens = np.diff(qs) if qs.size > 1 else np.zeros(0, dtype=np.int64)
     tiles = (lens + BLOCK_M - 1) // BLOCK_M
-    seqs = np.repeat(np.arange(lens.size, dtype=np.int32), tiles)
+    seqs = np.repeat(np.arange(lens.size, dtype=np.int64), tiles)
     first = np.repeat(np.cumsum(tiles) - tiles, tiles)
-    starts = ((np.arange(seqs.size) - first) * BLOCK_M).astype(np.int32)
+    starts = (np.arange(seqs.size) - first) * BLOCK_M
+    if context_lens_host is not None and seqs.size > 1:
+        ctx = np.asarray(context_lens_host, dtype=np.int64)
+        cost = np.minimum(ctx[seqs], ctx[seqs] - lens[seqs] + starts + BLOCK_M)
+        order = np.argsort(-cost, kind="stable")
+        half = (order.size + 1) // 2
+        order = np.concatenate([order[:half], order[half:][::-1]])
+        seqs, starts = seqs[order], starts[order]
     t = torch.from_numpy(np.stack([seqs, starts]).astype(np.int32)).to(device, non_blocking=True)
     return t[0], t[1]
 
@@ -57,7 +72,6 @@ def paged_prefill_attention(
     (built here when None). `out` (optional, not in the reference signature)
     receives the result in place.
     """
-    del context_lens_host  # the kernel reads context_lens on the device
     if q.dim() != 3:
         raise ValueError(f"q must be [Tp, H, D], got {tuple(q.shape)}")
     t, h, d = q.shape
@@ -78,7 +92,9 @@ def paged_prefill_attention(
             raise ValueError(f"{name} must be int32")
     if block_tables.dim() != 2 or block_tables.shape[0] != len(query_start_host) - 1:
         raise ValueError("block_tables must be [P, max_blocks]")
-    prog_seq, prog_m = programs if programs is not None else build_programs(query_start_host, q.device)
+    if programs is None:
+        programs = build_programs(query_start_host, q.device, context_lens_host)
+    prog_seq, prog_m = programs
     if prog_seq.numel() == 0:
         return out
     if q.stride(-1) != 1:

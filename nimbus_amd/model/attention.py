@@ -93,7 +93,8 @@ class AttentionBackend:
         p = meta.num_prefill_tokens
         if p:
             if meta.prefill_programs is None:
-                meta.prefill_programs = self._build_programs(meta.prefill_query_start_host, q.device)
+                meta.prefill_programs = self._build_programs(meta.prefill_query_start_host, q.device,
+                                                             meta.prefill_context_lens_host)
             self._prefill(
                 q[:p], k_cache, v_cache, meta.prefill_query_start, meta.prefill_context_lens,
                 meta.prefill_block_tables, scale, meta.prefill_query_start_host,

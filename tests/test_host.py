@@ -33,6 +33,22 @@ def test_build_programs_matches_reference_loop(qs):
     assert s.dtype == m.dtype == torch.int32
 
 
+@pytest.mark.parametrize("qs,ctx", [([0, 512, 1024, 1536, 2048], [700, 1536, 512, 1000]),
+                                    ([0, 5, 69, 72], [5, 100, 3]), ([0, 64], [64])])
+def test_build_programs_cost_order_keeps_the_entries(qs, ctx):
+    """With context lengths the table holds the reference's entries, heaviest
+    first with the lighter half reversed."""
+    s, m = prefill_attention.build_programs(qs, "cpu", ctx)
+    want = sorted(zip(*_programs_loop(qs)))
+    assert sorted(zip(s.tolist(), m.tolist())) == want
+    lens = [qs[i + 1] - qs[i] for i in range(len(ctx))]
+    cost = [min(ctx[a], ctx[a] - lens[a] + b + 64) for a, b in zip(s.tolist(), m.tolist())]
+    half = (len(cost) + 1) // 2
+    assert cost[:half] == sorted(cost[:half], reverse=True)
+    assert cost[half:] == sorted(cost[half:])
+    assert not cost[half:] or min(cost[:half]) >= max(cost[half:])
+
+
 def test_attn_metadata_fields_match_reference():
     # nimbus/model/attention.py:24-50, in order
     want = ["slot_mapping", "num_prefill_tokens", "prefill_query_start", "prefill_context_lens",
