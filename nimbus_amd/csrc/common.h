@@ -53,33 +53,26 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
 }
 
 // The prefill kernel's P.V product runs in fp16 whatever the cache dtype:
-// P lies in [0, 1], where fp16 keeps 3 more mantissa bits than bf16
+// P lies in [0, 256], where fp16 keeps 3 more mantissa bits than bf16
 // (rounding P to bf16 alone costs ~8e-3 at |o| ~ 0.5, beyond the output
-// tolerance), and a bf16 V element converts to fp16 exactly when
-// |v| <= 65504 (smaller magnitudes lose at most 2^-25 in fp16's subnormal
-// range). Larger |v| saturate to +-65504 rather than becoming inf, so one
-// outlier cannot turn masked-out products (0 * inf) into NaN for other rows.
-// (Decode, which cannot afford a per-element conversion of V, keeps V in
-// bf16 and splits P into two bf16 terms instead.)
-template <int DT>
-__device__ __forceinline__ uint16_t v_to_f16_bits(uint16_t x);
+// tolerance), and a finite bf16 V element converts to fp16 exactly when
+// |v| <= 65504 (smaller magnitudes lose at most 2^-24 in fp16's subnormal
+// range). The conversion rounds toward zero, so larger finite |v| saturate
+// to +-65504 rather than becoming inf, and one outlier cannot turn
+// masked-out products (0 * inf) into NaN for other rows. (Decode, which
+// cannot afford a per-element conversion of V, keeps V in bf16 and splits P
+// into two bf16 terms instead.)
 
-template <>
-__device__ __forceinline__ uint16_t v_to_f16_bits<kFloat16>(uint16_t x) {
-  return x;
-}
-
-template <>
-__device__ __forceinline__ uint16_t v_to_f16_bits<kBFloat16>(uint16_t x) {
-  float f = bf16_to_f32(x);
-  if (__builtin_fabsf(f) > 65504.f) f = __builtin_copysignf(65504.f, f);
-  return f32_to_f16(f);
+// Two fp32 values packed into one dword of fp16, rounded toward zero
+// (v_cvt_pkrtz_f16_f32: finite values beyond the fp16 range give +-65504).
+__device__ __forceinline__ uint32_t pack_f16_rtz(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
 }
 
 // Two 16-bit V elements packed in a dword, converted together: each half to
-// fp32 (a shift or a mask), clamped to the fp16 range with one med3, then
-// both packed by one v_cvt_pkrtz (exact for bf16 values in range, so the
-// conversion's rounding mode does not matter).
+// fp32 (a shift or a mask), then both packed by one v_cvt_pkrtz, which is
+// exact for bf16 values in the fp16 normal range and saturates finite values
+// beyond it.
 template <int DT>
 __device__ __forceinline__ uint32_t v_to_f16_pair(uint32_t w);
 
@@ -90,9 +83,7 @@ __device__ __forceinline__ uint32_t v_to_f16_pair<kFloat16>(uint32_t w) {
 
 template <>
 __device__ __forceinline__ uint32_t v_to_f16_pair<kBFloat16>(uint32_t w) {
-  const float lo = __builtin_amdgcn_fmed3f(__uint_as_float(w << 16), -65504.f, 65504.f);
-  const float hi = __builtin_amdgcn_fmed3f(__uint_as_float(w & 0xffff0000u), -65504.f, 65504.f);
-  return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(lo, hi));
+  return pack_f16_rtz(__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u));
 }
 
 template <int DT> struct Elem;

@@ -34,6 +34,8 @@
 //                                              with ds_read_b64_tr_b16, P^T is
 //                                              the QK output layout as is
 // Causal and context masks are applied only on blocks that need them.
+#include <type_traits>
+
 #include "common.h"
 #include "nimbus_attn_internal.h"
 
@@ -41,6 +43,7 @@ namespace nimbus {
 
 constexpr int kBlockN = 64;        // keys per iteration (four pages)
 constexpr float kLazyMax = 8.f;    // log2 headroom before the running max moves
+constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3: 32-bit data format, raw (unswizzled) access
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -71,6 +74,13 @@ struct PrefillShape {
   static constexpr int kSub = kPrefillTile / kPos;  // units per tile-table entry
 };
 
+// Waves per SIMD the register budget is sized for: two, except the
+// two-wave workgroups of GS = 1 at D = 128, whose staging registers double.
+template <int D, int GS>
+struct PrefillOccupancy {
+  static constexpr int kWavesPerEU = (GS == 1 && D == 128) ? 1 : 2;
+};
+
 // Swizzled 16-byte chunk positions of the LDS tiles. K rows are read sixteen
 // at a time (one key per lane column) by the QK operand loads; V rows sixteen
 // at a time by the transposed reads. XOR-ing the chunk index with a function
@@ -89,19 +99,29 @@ __device__ __forceinline__ int32_t scalar_load_i32(const int32_t* p, int i) {
   return ((const_ptr)(p))[i];
 }
 
+// Page ids of one 64-key block (four pages), range-checked.
+struct BlockPages {
+  int id[4];
+};
+
+template <int N>
+using IntC = std::integral_constant<int, N>;
+template <bool B>
+using BoolC = std::integral_constant<bool, B>;
+
 template <int DT, int D, int GS>
-__global__ __launch_bounds__(PrefillShape<GS>::kThreads) __attribute__((amdgpu_waves_per_eu(2))) void
-paged_prefill_kernel(PrefillArgs a) {
+__device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   using Shape = PrefillShape<GS>;
   constexpr int NT = Shape::kThreads;
   constexpr int POS = Shape::kPos;
   constexpr int KK = D / 32;                // 16x16x32 steps over the head dim (QK)
   constexpr int ND = D / 16;                // 16-row blocks of O^T
   constexpr int CPR = D / 8;                // 16-byte chunks per K/V row
-  constexpr int PIECES = kBlockN * CPR;     // 16-byte pieces in one K (or V) tile
-  constexpr int PPT = PIECES / NT;          // pieces per thread
+  constexpr int PPT = kBlockN * CPR / NT;   // 16-byte pieces per thread per tile
   constexpr int TILE = kBlockN * D;         // u16 elements of one tile
-  static_assert(PIECES % NT == 0, "tile pieces must divide evenly");
+  constexpr int KPW = 64 / CPR;             // keys one wave's 64 lanes cover per piece
+  constexpr int KSTEP = NT / CPR;           // keys between a thread's consecutive pieces
+  static_assert((kBlockN * CPR) % NT == 0 && 16 % KPW == 0, "tile pieces must divide evenly");
   __shared__ __attribute__((aligned(16))) uint16_t ks[2 * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t vs[2 * TILE];
 
@@ -123,7 +143,7 @@ paged_prefill_kernel(PrefillArgs a) {
   const int n_kb = (kv_end + kBlockN - 1) / kBlockN;
 
   const int tid = threadIdx.x;
-  const int wave = tid / 64;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64) & (Shape::kWaves - 1);  // scalar, range known
   const int lane = tid % 64;
   const int col = lane % 16;
   const int grp = lane / 16;
@@ -139,12 +159,9 @@ paged_prefill_kernel(PrefillArgs a) {
     qpos[nb] = base_pos + m0 + pos;
     head[nb] = kvh * a.G + gsub * GS + r % GS;
   }
-  // Keys this wave's rows can see: [0, wave_end); blocks wholly below
-  // wave_lo need no causal mask.
-  const int wave_pos_lo = (32 * wave) / GS;
-  const int wave_pos_hi = min((32 * wave + 31) / GS, q_len - 1 - m0);
-  const int wave_end = wave_pos_lo > q_len - 1 - m0 ? 0 : min(kv_end, base_pos + m0 + wave_pos_hi + 1);
-  const int wave_lo = base_pos + m0 + wave_pos_lo;
+  // Smallest position among this wave's rows: blocks wholly at or below it
+  // (and inside the context) need no mask.
+  const int wave_lo = base_pos + m0 + (32 * wave) / GS;
 
   // Q^T as the B operand (rows past q_len load the last query row).
   u32x4 qop[2][KK];
@@ -156,75 +173,98 @@ paged_prefill_kernel(PrefillArgs a) {
     for (int kk = 0; kk < KK; ++kk) qop[nb][kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * grp);
   }
 
+  // ---- staging
+  // Piece i of thread t is key lkey + KSTEP i, 16-byte slot lc of that LDS
+  // row. All of a wave's lanes fall in one page for a given i, so each load
+  // goes through a buffer resource (scalar registers) holding that page's
+  // address, plus a fixed 32-bit per-lane offset. The resource's size is the
+  // page's rows below kv_end, so keys past the context (in the last page, or
+  // in pages of a block beyond it) read as zeros: P is 0 there, and 0 * 0
+  // keeps garbage out of O. K goes global -> LDS directly
+  // (buffer_load_dwordx4 ... lds: lane l's 16 bytes land at the wave's LDS
+  // base + 16 l), so each lane loads the chunk that the swizzle puts in its
+  // slot; V passes through registers for the fp16 conversion.
   const int32_t* btrow = a.bt + seq * a.bt_sb;
-  const uint16_t* kbase = a.kc + static_cast<int64_t>(kvh) * a.c_sh;
-  const uint16_t* vbase = a.vc + static_cast<int64_t>(kvh) * a.c_sh;
   const int last_page = (kv_end + 15) / 16 - 1;
-
-  // Staging registers of one block: piece p = tid + NT * i is key p / CPR,
-  // chunk p % CPR.
-  u32x4 kreg[PPT], vreg[PPT];
-  auto load_block = [&](int kb) {
-    const int k0 = kb * kBlockN;
-    int pid[4];
+  auto load_pages = [&](int blk) {
+    int raw[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int page = min(k0 / 16 + i, last_page);
-      const int v = scalar_load_i32(btrow, page);
-      pid[i] = static_cast<uint32_t>(v) < static_cast<uint32_t>(a.num_blocks) ? v : 0;
-    }
+    for (int i = 0; i < 4; ++i) raw[i] = scalar_load_i32(btrow, min(4 * blk + i, last_page));
+    BlockPages p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p.id[i] = static_cast<uint32_t>(raw[i]) < static_cast<uint32_t>(a.num_blocks) ? raw[i] : 0;
+    return p;
+  };
+  const char* kbytes = reinterpret_cast<const char*>(a.kc + static_cast<int64_t>(kvh) * a.c_sh);
+  const char* vbytes = reinterpret_cast<const char*>(a.vc + static_cast<int64_t>(kvh) * a.c_sh);
+  const int64_t page_bytes = a.c_sb * 2;
+  const int row_bytes = static_cast<int>(a.c_st * 2);
+  const int lkey = tid / CPR;
+  const int lc = tid % CPR;
+  int k_goff[PPT], v_goff[PPT], v_st[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int key = lkey + KSTEP * i;
+    k_goff[i] = (key % 16) * row_bytes + 16 * k_pos<D>(key, lc);  // k_pos is an involution in the chunk index
+    v_goff[i] = (key % 16) * row_bytes + 16 * lc;
+    v_st[i] = key * D + 8 * v_pos<D>(key, lc);
+  }
+  // Buffer resource of the page holding piece i of this wave in block blk.
+  auto page_rsrc = [&](const char* base, const BlockPages& p, int blk, int i) {
+    const int j = (wave * KPW + KSTEP * i) / 16;
+    // (readfirstlane on each id keeps the select from being folded into an
+    // indexed load, which would put the ids in scratch memory)
+    const int p0 = __builtin_amdgcn_readfirstlane(p.id[0]), p1 = __builtin_amdgcn_readfirstlane(p.id[1]);
+    const int p2 = __builtin_amdgcn_readfirstlane(p.id[2]), p3 = __builtin_amdgcn_readfirstlane(p.id[3]);
+    const int id = (j & 2) ? ((j & 1) ? p3 : p2) : ((j & 1) ? p1 : p0);
+    // (readfirstlane keeps the clamp, which has no scalar form, from making
+    // the resource look divergent)
+    const int rows = __builtin_amdgcn_readfirstlane(min(max(kv_end - 16 * (4 * blk + j), 0), 16));
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + id * page_bytes, 0, rows * row_bytes,
+                                             kBufferFlags);
+  };
+  typedef __attribute__((address_space(3))) void lds_void;
+  auto dma_k = [&](const BlockPages& p, int blk, auto slot) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int p = tid + NT * i;
-      const int key = p / CPR;
-      const int c = p % CPR;
-      const int j = key / 16;
-      const int page_id = j == 0 ? pid[0] : j == 1 ? pid[1] : j == 2 ? pid[2] : pid[3];
-      const int64_t off = static_cast<int64_t>(page_id) * a.c_sb + (key % 16) * a.c_st + 8 * c;
-      kreg[i] = *reinterpret_cast<const u32x4*>(kbase + off);
-      vreg[i] = *reinterpret_cast<const u32x4*>(vbase + off);
+      uint16_t* dst = ks + slot * TILE + (wave * KPW + KSTEP * i) * D;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(page_rsrc(kbytes, p, blk, i), (lds_void*)dst, 16, k_goff[i], 0, 0, 0);
     }
   };
-  auto store_block = [&](int kb, int buf) {
-    const int k0 = kb * kBlockN;
-    const bool tail = k0 + kBlockN > kv_end;
+  u32x4 vreg[PPT];
+  auto issue_v = [&](const BlockPages& p, int blk) {
+#pragma unroll
+    for (int i = 0; i < PPT; ++i) vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(page_rsrc(vbytes, p, blk, i), v_goff[i], 0, 0);
+  };
+  auto store_v = [&](auto slot) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      const int p = tid + NT * i;
-      const int key = p / CPR;
-      const int c = p % CPR;
       u32x4 v = vreg[i];
-      // Keys past the context: P is 0 there, but 0 * garbage must not reach the sum.
-      if (tail && k0 + key >= kv_end) v = u32x4{0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = v_to_f16_pair<DT>(v[e]);
-      *reinterpret_cast<u32x4*>(ks + buf * TILE + key * D + 8 * k_pos<D>(key, c)) = kreg[i];
-      *reinterpret_cast<u32x4*>(vs + buf * TILE + key * D + 8 * v_pos<D>(key, c)) = v;
+      *reinterpret_cast<u32x4*>(vs + slot * TILE + v_st[i]) = v;
     }
   };
 
+  // ---- per-wave math
+  typedef f32x4 Scores[4][2];  // S^T of one block: [16-key block][16-row block]
   float m_run[2] = {-INFINITY, -INFINITY};
-  float l_lane[2] = {0.f, 0.f};
   f32x4 acc[ND][2];
+  f32x4 lsum[2];  // row sums of the fp16 P, accumulated by MFMA (all four lanes' values equal)
 #pragma unroll
-  for (int nd = 0; nd < ND; ++nd) {
-    acc[nd][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc[nd][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int nb = 0; nb < 2; ++nb) {
+    lsum[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
+  const u32x4 ones = u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};  // fp16 1.0
 
-  // Transposed-read addresses (see lds_read_tr16): lane j of group grp reads
-  // V row 16 mb + 4 grp + j/4, elements 16 nd + 4 (j%4) .. +4.
-  const int tr_row = 4 * grp + col / 4;
-  const int tr_half = 4 * ((col % 4) % 2);
-  const int tr_chunk = (col % 4) / 2;
-
-  auto compute_block = [&](int kb, int buf) {
-    const int k0 = kb * kBlockN;
-    const uint16_t* kt = ks + buf * TILE;
-    const uint16_t* vt = vs + buf * TILE;
-    f32x4 s[4][2];
+  // S^T[key][row] = K[key][:] . Q^T[:][row] for keys 32 h .. 32 h + 31.
+  auto qk = [&](auto slot, auto half, Scores& s) {
+    constexpr int H = decltype(half)::value;
+    const uint16_t* kt = ks + slot * TILE;
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb) {
+    for (int mb = 2 * H; mb < 2 * H + 2; ++mb) {
       s[mb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
       s[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
       const int key = 16 * mb + col;
@@ -235,8 +275,13 @@ paged_prefill_kernel(PrefillArgs a) {
         s[mb][1] = mfma_16x16x32<DT>(kop, qop[1][kk], s[mb][1]);
       }
     }
-    // Mask (raw scores; only blocks that reach past a row's position or the
-    // context need it), then lane-local maxima of the raw scores.
+  };
+  // Mask (raw scores; only blocks that reach past a row's position or the
+  // context need it), then the lazy running max (exp2 domain): it moves, and
+  // O and the row sums are rescaled, only when a score is more than
+  // 2^kLazyMax above it, so P <= 2^kLazyMax.
+  auto mask_and_max = [&](Scores& s, int blk) {
+    const int k0 = blk * kBlockN;
     const bool full = k0 + kBlockN - 1 <= wave_lo && k0 + kBlockN <= kv_end;
     if (!full) {
 #pragma unroll
@@ -260,76 +305,135 @@ paged_prefill_kernel(PrefillArgs a) {
       }
       lm[nb] = m * a.scale_log2;  // the scale is positive: max commutes with it
     }
-    // Lazy running max (exp2 domain): move it, and rescale O and the sums,
-    // only when a score is more than 2^kLazyMax above it; P <= 2^kLazyMax.
     if (__builtin_amdgcn_ballot_w64(lm[0] > m_run[0] + kLazyMax || lm[1] > m_run[1] + kLazyMax) != 0) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const float m_new = fmaxf(m_run[nb], max_across_groups(lm[nb]));
         const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[nb] - m_new);
         m_run[nb] = m_new;
-        l_lane[nb] *= alpha;
+        lsum[nb] *= alpha;
 #pragma unroll
         for (int nd = 0; nd < ND; ++nd) acc[nd][nb] *= alpha;
       }
     }
-    u32x4 pop[2][2];  // [key chunk of 32][row block]
+  };
+  // P^T = 2^(S^T * scale_log2 - m) for keys 32 h .. 32 h + 31 as fp16 B
+  // operands; a row with no score yet gives P = 0.
+  auto probs = [&](const Scores& s, auto half, u32x4 (&pop)[2]) {
+    constexpr int H = decltype(half)::value;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      // P = 2^(s * scale_log2 - m) in one FMA + exp; a row with no score yet gives P = 0.
       const float neg_m = m_run[nb] == -INFINITY ? 0.f : -m_run[nb];
-      uint16_t ph[4][4];
-      float sum = 0.f;
+      float p[2][4];
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
+      for (int j = 0; j < 2; ++j) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float p = fast_exp2(__builtin_fmaf(s[mb][nb][r], a.scale_log2, neg_m));
-          sum += p;
-          ph[mb][r] = f32_to_f16(p);
-        }
+        for (int r = 0; r < 4; ++r) p[j][r] = fast_exp2(__builtin_fmaf(s[2 * H + j][nb][r], a.scale_log2, neg_m));
       }
-      l_lane[nb] += sum;
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        pop[kc][nb] = u32x4{pack2(ph[2 * kc][0], ph[2 * kc][1]), pack2(ph[2 * kc][2], ph[2 * kc][3]),
-                            pack2(ph[2 * kc + 1][0], ph[2 * kc + 1][1]), pack2(ph[2 * kc + 1][2], ph[2 * kc + 1][3])};
-      }
-    }
-    // O^T[d][row] += V^T[d][key] P^T[key][row]
-#pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-#pragma unroll
-      for (int kc = 0; kc < 2; ++kc) {
-        const int r0 = 32 * kc + tr_row;
-        const int r1 = r0 + 16;
-        const u32x2 lo = lds_read_tr16(vt + r0 * D + 8 * v_pos<D>(r0, 2 * nd + tr_chunk) + tr_half);
-        const u32x2 hi = lds_read_tr16(vt + r1 * D + 8 * v_pos<D>(r1, 2 * nd + tr_chunk) + tr_half);
-        const u32x4 vop = u32x4{lo[0], lo[1], hi[0], hi[1]};
-        acc[nd][0] = mfma_16x16x32<kFloat16>(vop, pop[kc][0], acc[nd][0]);
-        acc[nd][1] = mfma_16x16x32<kFloat16>(vop, pop[kc][1], acc[nd][1]);
-      }
+      pop[nb] = u32x4{pack_f16_rtz(p[0][0], p[0][1]), pack_f16_rtz(p[0][2], p[0][3]), pack_f16_rtz(p[1][0], p[1][1]),
+                      pack_f16_rtz(p[1][2], p[1][3])};
     }
   };
+  // Transposed-read addresses (see lds_read_tr16): lane j of group grp reads
+  // V row 16 mb + 4 grp + j/4, elements 16 nd + 4 (j%4) .. +4.
+  const int tr_row = 4 * grp + col / 4;
+  const int tr_half = 4 * ((col % 4) % 2);
+  const int tr_chunk = (col % 4) / 2;
+  // O^T[d][row] += V^T[d][key] P^T[key][row]; row sums += 1^T P^T; keys
+  // 32 h .. 32 h + 31.
+  auto pv = [&](auto slot, auto half, const u32x4 (&pop)[2]) {
+    constexpr int H = decltype(half)::value;
+    const uint16_t* vt = vs + slot * TILE;
+    const int r0 = 32 * H + tr_row;
+    const int r1 = r0 + 16;
+#pragma unroll
+    for (int nd = 0; nd < ND; ++nd) {
+      const u32x2 lo = lds_read_tr16(vt + r0 * D + 8 * v_pos<D>(r0, 2 * nd + tr_chunk) + tr_half);
+      const u32x2 hi = lds_read_tr16(vt + r1 * D + 8 * v_pos<D>(r1, 2 * nd + tr_chunk) + tr_half);
+      const u32x4 vop = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      acc[nd][0] = mfma_16x16x32<kFloat16>(vop, pop[0], acc[nd][0]);
+      acc[nd][1] = mfma_16x16x32<kFloat16>(vop, pop[1], acc[nd][1]);
+    }
+    lsum[0] = mfma_16x16x32<kFloat16>(ones, pop[0], lsum[0]);
+    lsum[1] = mfma_16x16x32<kFloat16>(ones, pop[1], lsum[1]);
+  };
 
+  // ---- the block pipeline
+  // Iteration kb: the K tile of block kb + 1 and the V tile of block kb are
+  // in LDS (slots (kb + 1) & 1 and kb & 1), and S of block kb in registers.
+  // It issues the loads of V(kb + 1) and K(kb + 2), the latter straight into
+  // the slot K(kb) left (last read before the previous barrier); then, for
+  // each 32-key half, computes P(kb) while the QK products of block kb + 1
+  // run, and P(kb).V(kb); then it stores V(kb + 1) into the slot V(kb - 1)
+  // left, masks and takes the max of S(kb + 1), and meets the other waves at
+  // one barrier, which also waits for the K copies. The page ids of a block
+  // are read one iteration before its loads are issued.
+  Scores sa, sb;
+  BlockPages pg_v = load_pages(1);  // pages of V(kb + 1)
+  BlockPages pg_k = load_pages(2);  // pages of K(kb + 2)
   if (n_kb > 0) {
-    load_block(0);
-    store_block(0, 0);
-  }
-  __syncthreads();
-  for (int kb = 0; kb < n_kb; ++kb) {
-    const bool more = kb + 1 < n_kb;
-    if (more) load_block(kb + 1);  // in flight while this block is computed
-    if (kb * kBlockN < wave_end) compute_block(kb, kb & 1);
-    if (more) store_block(kb + 1, (kb + 1) & 1);
+    const BlockPages pg0 = load_pages(0);
+    issue_v(pg0, 0);
+    dma_k(pg0, 0, IntC<0>{});
     __syncthreads();
+    dma_k(pg_v, 1, IntC<1>{});  // past the context: zeros
+    qk(IntC<0>{}, IntC<0>{}, sa);
+    qk(IntC<0>{}, IntC<1>{}, sa);
+    store_v(IntC<0>{});
+    mask_and_max(sa, 0);
+    __syncthreads();
+  }
+  auto iteration = [&](int kb, auto slot, auto has_k2, auto has_next, Scores& s_cur, Scores& s_nxt) {
+    constexpr int SLOT = decltype(slot)::value;
+    constexpr bool K2 = decltype(has_k2)::value;
+    constexpr bool NEXT = decltype(has_next)::value;
+    BlockPages pg_n;
+    if constexpr (NEXT) issue_v(pg_v, kb + 1);
+    if constexpr (K2) {
+      pg_n = load_pages(kb + 3);
+      dma_k(pg_k, kb + 2, IntC<SLOT>{});
+    }
+    {
+      u32x4 pop[2];
+      probs(s_cur, IntC<0>{}, pop);
+      if constexpr (NEXT) qk(IntC<1 - SLOT>{}, IntC<0>{}, s_nxt);
+      pv(IntC<SLOT>{}, IntC<0>{}, pop);
+    }
+    {
+      u32x4 pop[2];
+      probs(s_cur, IntC<1>{}, pop);
+      if constexpr (NEXT) qk(IntC<1 - SLOT>{}, IntC<1>{}, s_nxt);
+      pv(IntC<SLOT>{}, IntC<1>{}, pop);
+    }
+    if constexpr (NEXT) {
+      store_v(IntC<1 - SLOT>{});
+      mask_and_max(s_nxt, kb + 1);
+      __syncthreads();
+    }
+    pg_v = pg_k;
+    if constexpr (K2) pg_k = pg_n;
+  };
+  int kb = 0;
+  for (; kb + 3 < n_kb; kb += 2) {
+    iteration(kb, IntC<0>{}, BoolC<true>{}, BoolC<true>{}, sa, sb);
+    iteration(kb + 1, IntC<1>{}, BoolC<true>{}, BoolC<true>{}, sb, sa);
+  }
+  // kb is even here; 0 to 3 iterations remain.
+  if (kb + 2 < n_kb) {
+    iteration(kb, IntC<0>{}, BoolC<true>{}, BoolC<true>{}, sa, sb);
+    iteration(kb + 1, IntC<1>{}, BoolC<false>{}, BoolC<true>{}, sb, sa);
+    iteration(kb + 2, IntC<0>{}, BoolC<false>{}, BoolC<false>{}, sa, sb);
+  } else if (kb + 1 < n_kb) {
+    iteration(kb, IntC<0>{}, BoolC<false>{}, BoolC<true>{}, sa, sb);
+    iteration(kb + 1, IntC<1>{}, BoolC<false>{}, BoolC<false>{}, sb, sa);
+  } else if (kb < n_kb) {
+    iteration(kb, IntC<0>{}, BoolC<false>{}, BoolC<false>{}, sa, sb);
   }
 
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    const float l = sum_across_groups(l_lane[nb]);
     if (!row_ok[nb]) continue;
-    const float inv = 1.f / l;
+    const float inv = 1.f / lsum[nb][0];
     const int pos = (32 * wave + 16 * nb + col) / GS;
     uint16_t* orow = a.out + static_cast<int64_t>(qs + m0 + pos) * a.o_st + static_cast<int64_t>(head[nb]) * a.o_sh;
 #pragma unroll
@@ -342,13 +446,31 @@ paged_prefill_kernel(PrefillArgs a) {
   }
 }
 
+// One kernel per register budget (the occupancy attribute takes a constant).
+template <int DT, int D, int GS>
+__global__ __launch_bounds__(PrefillShape<GS>::kThreads) __attribute__((amdgpu_waves_per_eu(2))) void
+paged_prefill_kernel(PrefillArgs a) {
+  prefill_unit<DT, D, GS>(a);
+}
+
+template <int DT, int D, int GS>
+__global__ __launch_bounds__(PrefillShape<GS>::kThreads) __attribute__((amdgpu_waves_per_eu(1))) void
+paged_prefill_kernel_1w(PrefillArgs a) {
+  prefill_unit<DT, D, GS>(a);
+}
+
 template <int DT, int D, int GS>
 static int launch_prefill(const PrefillArgs& a, int num_programs, hipStream_t stream) {
   using Shape = PrefillShape<GS>;
   const int64_t units = static_cast<int64_t>(num_programs) * Shape::kSub * a.kvg;
   if (units > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
-  hipLaunchKernelGGL((paged_prefill_kernel<DT, D, GS>), dim3(static_cast<unsigned>(units)), dim3(Shape::kThreads), 0,
-                     stream, a);
+  if constexpr (PrefillOccupancy<D, GS>::kWavesPerEU == 1) {
+    hipLaunchKernelGGL((paged_prefill_kernel_1w<DT, D, GS>), dim3(static_cast<unsigned>(units)),
+                       dim3(Shape::kThreads), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, GS>), dim3(static_cast<unsigned>(units)), dim3(Shape::kThreads),
+                       0, stream, a);
+  }
   return static_cast<int>(hipGetLastError());
 }
 
@@ -391,6 +513,9 @@ extern "C" int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q
   if (!q || !k_cache || !v_cache || !block_tables || !query_start || !context_lens || !prog_seq || !prog_m || !out)
     return NIMBUS_ERR_INVALID;
   if (num_blocks <= 0 || num_blocks > INT32_MAX || bt_width <= 0) return NIMBUS_ERR_INVALID;
+  // Pages are read through buffer resources with 32-bit offsets: 16 token
+  // rows of a page must span less than 2 GiB.
+  if (cache_stride_token <= 0 || cache_stride_token > (int64_t{1} << 25)) return NIMBUS_ERR_UNSUPPORTED;
   if ((q_stride_t | q_stride_h | cache_stride_block | cache_stride_token | cache_stride_head | out_stride_t |
        out_stride_h) % 8 != 0)
     return NIMBUS_ERR_ALIGNMENT;
