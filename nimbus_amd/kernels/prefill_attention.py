@@ -17,6 +17,9 @@ from nimbus_amd import _lib
 from nimbus_amd.kernels.paged_attention import _check_cache
 
 BLOCK_M = 64  # query positions per tile-table entry (NIMBUS_PREFILL_TILE)
+# Tiles whose workgroups all fit the chip at once: a GQA tile is typically 16
+# workgroups (kv-head groups x sub-tiles), and 256 CUs hold two each.
+PAIRED_TILES = 32
 
 
 def build_programs(query_start_host: list[int], device,
@@ -30,10 +33,15 @@ def build_programs(query_start_host: list[int], device,
     (model/attention.py:82-83).
 
     With context_lens_host (not in the reference signature; the backend
-    passes it) the same entries are ordered for the MI355X launch: by cost
-    (the keys the tile's last query sees), heaviest first, and the lighter
-    half reversed, so that workgroups launched half a grid apart, which
-    share a CU, pair a heavy tile with a light one.
+    passes it) the same entries are ordered for the MI355X launch. A tile's
+    cost is the keys its last query sees. Sequences go heaviest first (by
+    the sum of their tiles' costs), each sequence's tiles together and
+    heaviest first: tiles of one sequence read the same K/V pages, so
+    keeping them adjacent keeps them resident together and their pages in
+    L2, and a longer table ends on light tiles. A table short enough that
+    all its workgroups start at once (at most PAIRED_TILES tiles) has its
+    second half reversed instead, so that workgroups launched half a grid
+    apart, which share a CU, pair a heavy tile with a light one.
     """
     qs = np.asarray(query_start_host, dtype=np.int64)
     lens = np.diff(qs) if qs.size > 1 else np.zeros(0, dtype=np.int64)
@@ -44,9 +52,11 @@ def build_programs(query_start_host: list[int], device,
     if context_lens_host is not None and seqs.size > 1:
         ctx = np.asarray(context_lens_host, dtype=np.int64)
         cost = np.minimum(ctx[seqs], ctx[seqs] - lens[seqs] + starts + BLOCK_M)
-        order = np.argsort(-cost, kind="stable")
-        half = (order.size + 1) // 2
-        order = np.concatenate([order[:half], order[half:][::-1]])
+        seq_cost = np.bincount(seqs, weights=cost, minlength=lens.size)[seqs]
+        order = np.lexsort((-cost, seqs, -seq_cost))  # last key is the primary one
+        if order.size <= PAIRED_TILES:
+            half = (order.size + 1) // 2
+            order = np.concatenate([order[:half], order[half:][::-1]])
         seqs, starts = seqs[order], starts[order]
     t = torch.from_numpy(np.stack([seqs, starts]).astype(np.int32)).to(device, non_blocking=True)
     return t[0], t[1]

@@ -34,19 +34,31 @@ def test_build_programs_matches_reference_loop(qs):
 
 
 @pytest.mark.parametrize("qs,ctx", [([0, 512, 1024, 1536, 2048], [700, 1536, 512, 1000]),
-                                    ([0, 5, 69, 72], [5, 100, 3]), ([0, 64], [64])])
+                                    ([0, 5, 69, 72], [5, 100, 3]), ([0, 64], [64]),
+                                    ([0] + [512 * (i + 1) for i in range(6)], [2560] * 6),
+                                    ([0] + [200 * (i + 1) for i in range(12)], [300 + 50 * i for i in range(12)])])
 def test_build_programs_cost_order_keeps_the_entries(qs, ctx):
-    """With context lengths the table holds the reference's entries, heaviest
-    first with the lighter half reversed."""
+    """With context lengths the table holds the reference's entries: sequences
+    heaviest first, each sequence's tiles adjacent and heaviest first, and,
+    for a table short enough to start at once, the second half reversed."""
     s, m = prefill_attention.build_programs(qs, "cpu", ctx)
-    want = sorted(zip(*_programs_loop(qs)))
-    assert sorted(zip(s.tolist(), m.tolist())) == want
+    got = list(zip(s.tolist(), m.tolist()))
+    entries = _programs_loop(qs)
+    assert sorted(got) == sorted(zip(*entries))
     lens = [qs[i + 1] - qs[i] for i in range(len(ctx))]
-    cost = [min(ctx[a], ctx[a] - lens[a] + b + 64) for a, b in zip(s.tolist(), m.tolist())]
-    half = (len(cost) + 1) // 2
-    assert cost[:half] == sorted(cost[:half], reverse=True)
-    assert cost[half:] == sorted(cost[half:])
-    assert not cost[half:] or min(cost[:half]) >= max(cost[half:])
+    cost = {(a, b): min(ctx[a], ctx[a] - lens[a] + b + 64) for a, b in zip(*entries)}
+    seq_cost = {a: sum(c for (x, _), c in cost.items() if x == a) for a in range(len(ctx))}
+    half = (len(got) + 1) // 2
+    paired = len(got) <= prefill_attention.PAIRED_TILES
+    listed = got[:half] + got[half:][::-1] if paired else got
+    keys = [(-seq_cost[a], a, -cost[(a, b)]) for a, b in listed]
+    assert keys == sorted(keys)
+    # each sequence's tiles stay together in the listed order
+    seen = []
+    for a, _ in listed:
+        if not seen or seen[-1] != a:
+            assert a not in seen
+            seen.append(a)
 
 
 def test_attn_metadata_fields_match_reference():
