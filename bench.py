@@ -24,6 +24,9 @@ prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
              the 2.5 PFLOP/s dense bf16 MFMA peak
 mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
              (eager) + the 60 decodes replayed from a hipGraph padded to 64
+add_rms_norm the fused residual add + RMSNorm at three model shapes:
+             algorithmic bytes (x and residual read, residual and output
+             written, weight once) / mean kernel time, against 8 TB/s
 
 Between timed calls the K/V pool rotates over enough copies (>= 1.5 GB) that
 the 256 MB Infinity Cache cannot serve one call's pages to the next.
@@ -284,6 +287,54 @@ def time_mixed_step(batch, steps, warmup):
             "padded_batch": gb, "tokens": int(batch.q.shape[0])}
 
 
+# ---------------------------------------------------------------- fused residual add + RMSNorm
+
+NORM_SHAPES = (
+    ("tinyllama: 2048 tokens x 2048, fp16 (Nimbus's own bench shape)", 2048, 2048, "float16"),
+    ("llama3 config-4 step: 2108 tokens x 4096, bf16", 2108, 4096, "bfloat16"),
+    ("llama3 decode: 64 tokens x 4096, bf16", 64, 4096, "bfloat16"),
+)
+
+
+def time_add_rms_norm(steps, warmup):
+    """add_rms_norm at the model shapes: algorithmic bytes (read x and the
+    residual, write the new residual and the output, the weight once) per
+    kernel time, against HBM peak. The calls are captured back to back in a
+    hipGraph (one per pool of inputs, the pools covering >= 256 MB so the
+    Infinity Cache does not hold a call's rows) and the graph is replayed, so
+    the time is the kernels', not the Python launch path's."""
+    import torch
+
+    from nimbus_amd.kernels.rmsnorm import add_rms_norm
+
+    res = []
+    for name, rows, cols, dt in NORM_SHAPES:
+        dtype = getattr(torch, dt)
+        nbytes = 4 * rows * cols * 2 + cols * 2
+        n_pools = max(8, int(math.ceil(256e6 / (2 * rows * cols * 2))))
+        g = torch.Generator(device="cuda").manual_seed(rows)
+        pools = [(torch.randn(rows, cols, generator=g, device="cuda").to(dtype),
+                  torch.randn(rows, cols, generator=g, device="cuda").to(dtype)) for _ in range(n_pools)]
+        w = torch.randn(cols, generator=g, device="cuda").to(dtype)
+        for x, r in pools[:2]:
+            add_rms_norm(x, r, w, 1e-5)  # load the library, warm the caches
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for x, r in pools:
+                add_rms_norm(x, r, w, 1e-5)
+        for i in range(warmup):
+            graph.replay()
+        per_replay = statistics.mean(event_times_us(lambda i: graph.replay(), max(3, steps // 10),
+                                                    torch.cuda.current_stream()))
+        us = per_replay / n_pools
+        res.append({"shape": name, "rows": rows, "cols": cols, "dtype": dt, "us_per_call": us, "bytes": nbytes,
+                    "GBps": nbytes / us / 1e3, "frac_hbm_peak": nbytes / us / 1e3 / HBM_PEAK_GBS,
+                    "calls_per_replay": n_pools})
+        del graph, pools
+    return res
+
+
 # ---------------------------------------------------------------- --all
 
 def all_configs(steps, warmup):
@@ -388,6 +439,10 @@ def main(argv=None):
         result["mixed_step"] = time_mixed_step(mixed, args.steps, args.warmup)
         log(f"prefill: {result['prefill']}  mixed: {result['mixed_step']}")
         del mixed
+    if not args.no_prefill:
+        log("add_rms_norm")
+        result["add_rms_norm"] = time_add_rms_norm(args.steps, args.warmup)
+        log(f"add_rms_norm: {result['add_rms_norm']}")
     if args.all:
         result["configs"] = {k: {a: b for a, b in v.items() if not isinstance(b, dict)}
                              for k, v in all_configs(args.steps, args.warmup).items()}

@@ -3,7 +3,7 @@
  *
  * libnimbus_attn.so replaces the GPU side of Nimbus's attention hot path:
  * the KV slot write, paged decode attention and causal varlen paged prefill
- * attention. Every entry point takes plain device pointers, element strides
+ * attention, and the fused residual add + RMSNorm on either side of it. Every entry point takes plain device pointers, element strides
  * (not bytes), sizes, a dtype code and an opaque hipStream_t; none allocates,
  * frees, synchronises or reads device memory on the host, so each call can be
  * recorded into a hipGraph. PyTorch (or any caller) owns every buffer.
@@ -25,7 +25,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 2
+#define NIMBUS_ATTN_ABI_VERSION 3
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -143,6 +143,21 @@ int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, 
                          int32_t num_programs, void* out, int64_t out_stride_t, int64_t out_stride_h,
                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
                          int32_t dtype, void* stream);
+
+/*
+ * Fused residual add + RMSNorm. Replaces nimbus/kernels/rmsnorm.py:21-59
+ * (the Triton _rmsnorm_kernel behind rms_norm and add_rms_norm), with the
+ * numerics of nimbus/kernels/reference.py:99-112:
+ *   s = x + residual (in the element type; written to residual_out),
+ *   out = weight * dtype(s * rsqrt(mean(s^2) + eps)) (mean and scale in fp32).
+ * residual == NULL is plain RMSNorm of x (residual_out unused). Rows are
+ * [rows, cols] with unit element stride and the given row strides; cols must
+ * be a multiple of 8 and at most 8192.
+ */
+int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
+                        const void* weight, void* out, int64_t out_stride, void* residual_out,
+                        int64_t residual_out_stride, int64_t rows, int32_t cols, float eps, int32_t dtype,
+                        void* stream);
 
 #ifdef __cplusplus
 }

@@ -103,3 +103,10 @@ def write_kv(k, v, k_cache, v_cache, slot_mapping):
     kc.reshape(nb * bs, kv, d)[slots] = _np(k)
     vc.reshape(nb * bs, kv, d)[slots] = _np(v)
     return kc, vc
+
+
+def rms_norm(x, weight, eps):
+    """float64 RMSNorm from the definition: w * x / sqrt(mean(x^2) + eps), per row."""
+    xf = _np(x).astype(np.float64)
+    w = _np(weight).astype(np.float64)
+    return w * xf / np.sqrt(np.mean(xf * xf, axis=-1, keepdims=True) + eps)

@@ -12,11 +12,14 @@ Each function follows one function of the reference, op for op:
   decode_attention_rows   same mathematics as :71-96, one sequence at a time,
                           for batches whose padded gather does not fit in host
                           memory (~34 GB batched)
+  rms_norm                nimbus/kernels/reference.py:99-104
+  add_rms_norm            nimbus/kernels/reference.py:107-112
 
 Pinned by tests/test_oracle.py against oracle.closed_form (float64 brute force)
 and against special cases with textbook answers (ctx=1 gives v_0; one-hot
 scores select one row of V; uniform scores average V; the slot write is a
-NumPy scatter).
+NumPy scatter; a constant row normalises to +-1; the residual add is NumPy's
+element-type addition).
 """
 
 from __future__ import annotations
@@ -110,3 +113,24 @@ def decode_attention_rows(q, k_cache, v_cache, context_lens_host, block_tables, 
         o = F.scaled_dot_product_attention(q[b][None, :, None, :], kb, vb, scale=scale, enable_gqa=True)
         out[b] = o[0, :, 0, :]
     return out
+
+
+def rms_norm(x, weight, eps: float):
+    """HuggingFace LlamaRMSNorm order of operations.
+
+    Follows nimbus/kernels/reference.py:99-104: normalise in float32, cast
+    back to x's dtype, then multiply by the weight in that dtype.
+    """
+    dtype = x.dtype
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * xf.to(dtype)
+
+
+def add_rms_norm(x, residual, weight, eps: float):
+    """residual + x in the model dtype, then rms_norm of it; returns (norm, residual).
+
+    Follows nimbus/kernels/reference.py:107-112.
+    """
+    residual = residual + x
+    return rms_norm(residual, weight, eps), residual

@@ -23,7 +23,8 @@ def declared_functions() -> list[str]:
 def test_header_declares_the_four_launch_paths():
     names = declared_functions()
     for want in ("nimbus_write_kv", "nimbus_paged_decode", "nimbus_paged_decode_workspace_bytes",
-                 "nimbus_paged_prefill", "nimbus_attn_abi_version", "nimbus_attn_error_string"):
+                 "nimbus_paged_prefill", "nimbus_add_rms_norm", "nimbus_attn_abi_version",
+                 "nimbus_attn_error_string"):
         assert want in names
 
 
@@ -111,3 +112,15 @@ def test_prefill_and_write_kv_argument_checks():
     wk[13] = 3
     wk[5] = 5
     assert lib.nimbus_write_kv(*wk) == _lib.NIMBUS_ERR_UNSUPPORTED
+
+
+def test_rms_norm_rejects_before_launch():
+    """Shapes outside the kernel and null pointers return an error code; no
+    pointer is dereferenced on the host, so null is safe to pass here."""
+    lib = _lib.load()
+    f = lib.nimbus_add_rms_norm
+    for cols in (12, 0, 8200, 16384):  # not a multiple of 8, empty, too long
+        assert f(None, 0, None, 0, None, None, 0, None, 0, 4, cols, 1e-5, 0, None) in (-1, -2)
+    assert f(None, 0, None, 0, None, None, 0, None, 0, 4, 16, 1e-5, 7, None) == -2  # dtype
+    assert f(None, 0, None, 0, None, None, 0, None, 0, 4, 16, 1e-5, 0, None) == -1  # null x
+    assert f(None, 0, None, 0, None, None, 0, None, 0, 0, 16, 1e-5, 0, None) == 0  # no rows: nothing to do

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from nimbus_amd import workloads
-from nimbus_amd.kernels import cache_ops, paged_attention, prefill_attention
+from nimbus_amd.kernels import cache_ops, paged_attention, prefill_attention, rmsnorm
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
 
 
@@ -86,6 +86,19 @@ def test_kernels_refuse_cpu_tensors():
                                                   bt[:1], 0.125, [0, 2], [2])
     with pytest.raises(ValueError, match="GPU"):
         cache_ops.write_kv(q[:, :2], q[:, :2], k, k, torch.zeros(2, dtype=torch.int64))
+    x = torch.zeros(3, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        rmsnorm.add_rms_norm(x, x, torch.ones(64, dtype=torch.float16), 1e-5)
+
+
+def test_rms_norm_wrapper_checks_shapes():
+    x = torch.zeros(3, 60, dtype=torch.float16)
+    with pytest.raises(NotImplementedError):
+        rmsnorm.rms_norm(x, torch.ones(60, dtype=torch.float16), 1e-5)
+    with pytest.raises(NotImplementedError):
+        rmsnorm.rms_norm(torch.zeros(2, 64), torch.ones(64), 1e-5)  # float32
+    with pytest.raises(ValueError):
+        rmsnorm.rms_norm(torch.zeros(2, 64, dtype=torch.float16), torch.ones(32, dtype=torch.float16), 1e-5)
 
 
 def test_batch_layout_follows_runner():

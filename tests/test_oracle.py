@@ -271,3 +271,67 @@ def test_planted_prefill_mistakes_are_caught(kind):
     assert max_violation(reference.paged_prefill_attention(*args), want) <= 0
     bad = _mutant_prefill(kind, q, k, v, qs, ctx_lens, bt, scale)
     assert not (max_violation(torch.nan_to_num(bad, nan=1e9), want) <= 0), kind
+
+
+# ---------------------------------------------------------------- fused residual add + RMSNorm
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_add_rms_norm_residual_is_the_element_type_add(dtype):
+    """The new residual is x + r rounded once to the element type (NumPy's
+    float16 addition is IEEE; bf16 is checked through float32, where the
+    exact sum of two bf16 values fits)."""
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(7, 256, generator=g) * 3).to(dtype)
+    r = (torch.randn(7, 256, generator=g) * 3).to(dtype)
+    w = torch.randn(256, generator=g).to(dtype)
+    _, res = reference.add_rms_norm(x, r, w, 1e-5)
+    if dtype == torch.float16:
+        want = (x.numpy() + r.numpy()).astype(np.float16)
+        assert np.array_equal(res.numpy().view(np.uint16), want.view(np.uint16))
+    else:
+        want = (x.float() + r.float()).to(torch.bfloat16)
+        assert torch.equal(res.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 2048), (37, 2048), (5, 768), (3, 4096)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_rms_norm_oracle_matches_float64(rows, cols, dtype):
+    """The restated norm (float32 normalise, two roundings to the element
+    type) is within a few element-type ulps of the float64 definition."""
+    g = torch.Generator().manual_seed(rows * 31 + cols)
+    x = torch.randn(rows, cols, generator=g).to(dtype)
+    w = torch.randn(cols, generator=g).to(dtype)
+    got = reference.rms_norm(x, w, 1e-5).float().numpy()
+    want = closed_form.rms_norm(x, w, 1e-5)
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    assert np.all(np.abs(got - want) <= 2 * ulp * np.abs(want) + 1e-6)
+
+
+def test_rms_norm_of_a_constant_row_is_its_sign():
+    """mean(x^2) = c^2, so x / sqrt(c^2 + eps) = sign(c) (for eps << c^2)."""
+    x = torch.tensor([[2.5] * 64, [-0.75] * 64], dtype=torch.float16)
+    w = torch.ones(64, dtype=torch.float16)
+    got = reference.rms_norm(x, w, 1e-6)
+    assert torch.equal(got[0], torch.ones(64, dtype=torch.float16))
+    assert torch.equal(got[1], -torch.ones(64, dtype=torch.float16))
+    assert np.allclose(closed_form.rms_norm(x, w, 1e-6), np.sign(x.float().numpy()), atol=1e-6)
+
+
+@pytest.mark.parametrize("kind", ["no_eps", "wrong_axis", "weight_before_cast_missing", "sum_not_mean"])
+def test_planted_rms_norm_mistakes_are_caught(kind):
+    """The float64 check rejects plausible slips in the norm."""
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(6, 64, generator=g, dtype=torch.float32)
+    w = torch.randn(64, generator=g, dtype=torch.float32)
+    eps = 0.5  # large enough that dropping it shows
+    if kind == "no_eps":
+        bad = w * x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True))
+    elif kind == "wrong_axis":
+        bad = w * x * torch.rsqrt(x.pow(2).mean(0, keepdim=True) + eps)
+    elif kind == "weight_before_cast_missing":
+        bad = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    else:
+        bad = w * x * torch.rsqrt(x.pow(2).sum(-1, keepdim=True) + eps)
+    want = closed_form.rms_norm(x, w, eps)
+    assert np.allclose(reference.rms_norm(x, w, eps).numpy(), want, atol=1e-5)
+    assert not np.allclose(bad.numpy(), want, atol=1e-3)
