@@ -24,6 +24,9 @@ prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
              the 2.5 PFLOP/s dense bf16 MFMA peak
 mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
              (eager) + the 60 decodes replayed from a hipGraph padded to 64
+verify       speculative verification's attention (16 sequences x 5 tokens)
+             replayed from a hipGraph, with the decode kernel on the same
+             contexts beside it
 add_rms_norm the fused residual add + RMSNorm at three model shapes:
              algorithmic bytes (x and residual read, residual and output
              written, weight once) / mean kernel time, against 8 TB/s
@@ -287,6 +290,54 @@ def time_mixed_step(batch, steps, warmup):
             "padded_batch": gb, "tokens": int(batch.q.shape[0])}
 
 
+# ---------------------------------------------------------------- speculative verification
+
+def time_verify(steps, warmup, n=16, k=4):
+    """Speculative verification's attention (nimbus/spec/engine.py:60-150):
+    n sequences of k + 1 new tokens on Llama-3-8B-shaped contexts (log-uniform
+    128..8192), slot write + prefill replayed from a hipGraph. Bytes: every
+    visible K/V row once per kv head, the new tokens' K/V written and q/out.
+    The paged decode call on the same contexts (one token each) is timed
+    beside it as the bandwidth reference."""
+    import torch
+
+    from nimbus_amd import workloads
+    from nimbus_amd.graphs import VerifyAttentionGraphs
+    from nimbus_amd.kernels.paged_attention import (decode_workspace_bytes, new_decode_workspace,
+                                                    paged_decode_attention)
+
+    q_len = k + 1
+    ctx = workloads.llama3_decode_lens(seed=7, batch=n)
+    b = workloads.build_batch([(c, q_len) for c in ctx], heads=32, kv_heads=8, head_dim=128,
+                              dtype=torch.bfloat16, device="cuda", seed=7, pool_factor=1.2, write_first=False)
+    nb = b.k_cache.shape[0]
+    kc = torch.cat([b.k_cache, torch.zeros_like(b.k_cache[:1])])
+    vc = torch.cat([b.v_cache, torch.zeros_like(b.v_cache[:1])])
+    graphs = VerifyAttentionGraphs(kc, vc, num_heads=32, scale=b.scale, max_model_len=8192, max_batch=n, k=k,
+                                   scratch_block=nb)
+    graphs.capture()
+    pa = b.prefill_args()
+    gb = graphs.load(b.q, b.k, b.v, b.slot_mapping, pa[4], b.block_tables)
+    for _ in range(warmup):
+        graphs.replay(gb)
+    us = statistics.mean(event_times_us(lambda i: graphs.replay(gb), steps, torch.cuda.current_stream()))
+    kv_bytes = sum(ctx) * 2 * 8 * 128 * 2
+    nbytes = kv_bytes + 2 * n * q_len * 32 * 128 * 2 + 2 * n * q_len * 8 * 128 * 2 * 2
+    # the decode kernel over the same contexts
+    qd = torch.randn(n, 32, 128, device="cuda").bfloat16()
+    ws = new_decode_workspace(decode_workspace_bytes(n, 32, 128, max(ctx)), torch.device("cuda"))
+    outd = torch.empty_like(qd)
+    for _ in range(warmup):
+        paged_decode_attention(qd, kc, vc, pa[4], b.block_tables, max(ctx), b.scale, out=outd, workspace=ws)
+    dus = statistics.mean(event_times_us(
+        lambda i: paged_decode_attention(qd, kc, vc, pa[4], b.block_tables, max(ctx), b.scale, out=outd,
+                                         workspace=ws), steps, torch.cuda.current_stream()))
+    return {"workload": f"{n} sequences x {q_len} tokens (k={k}), Llama-3-8B shape, contexts log-uniform "
+                        f"[128, 8192] (sum {sum(ctx)})", "us_per_replay": us, "bytes": nbytes,
+            "GBps": nbytes / us / 1e3, "decode_same_contexts_us": dus,
+            "decode_same_contexts_GBps": (kv_bytes + 2 * n * 32 * 128 * 2) / dus / 1e3}
+
+
 # ---------------------------------------------------------------- fused residual add + RMSNorm
 
 NORM_SHAPES = (
@@ -440,6 +491,9 @@ def main(argv=None):
         log(f"prefill: {result['prefill']}  mixed: {result['mixed_step']}")
         del mixed
     if not args.no_prefill:
+        log("speculative verify")
+        result["verify"] = time_verify(args.steps, args.warmup)
+        log(f"verify: {result['verify']}")
         log("add_rms_norm")
         result["add_rms_norm"] = time_add_rms_norm(args.steps, args.warmup)
         log(f"add_rms_norm: {result['add_rms_norm']}")

@@ -1,4 +1,5 @@
-"""Decode attention replayed from hipGraphs at padded batch sizes.
+"""Decode and speculative-verify attention replayed from hipGraphs at padded
+batch sizes.
 
 Follows the capture contract of Nimbus's DecodeGraphs (nimbus/cuda_graph.py:
 38-79 and 118-144), restricted to the attention layer (the slot write plus
@@ -14,6 +15,10 @@ paged decode attention) instead of the whole model:
 
 Nothing inside a captured region allocates outside the graph pool, reads
 device memory on the host or issues a memset.
+
+VerifyAttentionGraphs does the same for speculative verification
+(nimbus/spec/engine.py:60-150): there every sequence feeds k + 1 tokens, all
+through the prefill kernel.
 """
 
 from __future__ import annotations
@@ -118,3 +123,121 @@ class DecodeAttentionGraphs:
         """One decode attention step: returns [n, H, D] for the n real rows."""
         n = q.shape[0]
         return self.replay(self.load(q, k, v, slot_mapping, context_lens, block_tables))[:n]
+
+
+VERIFY_SIZES = (1, 2, 4, 8, 16)
+
+
+class VerifyAttentionGraphs:
+    """Speculative verification's attention replayed from hipGraphs.
+
+    Follows Nimbus's VerifyGraphs (nimbus/spec/engine.py:60-150), restricted
+    to the attention layer (slot write + paged prefill attention):
+
+    - every sequence feeds exactly q = k + 1 <= block_size tokens, all of
+      them prefill tokens, so a step's metadata differs only in device data;
+    - the tile table is precomputed as (arange(b), zeros(b)) (:86-87): one
+      entry per sequence, since q <= 16 < BLOCK_M;
+    - the host lists are placeholders ([q] * b context lengths, :96) that the
+      kernels never read: context lengths and query starts come from the
+      device buffers each replay;
+    - padding sequences (up to the captured sizes 1, 2, 4, 8, 16 below
+      max_batch, then max_batch) have context q and write and read the
+      scratch block, which holds q <= block_size tokens (:118-126).
+    """
+
+    def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, num_heads: int, scale: float,
+                 max_model_len: int, max_batch: int, k: int, scratch_block: int):
+        self.block_size = k_cache.shape[1]
+        if not 0 < k + 1 <= self.block_size:
+            raise ValueError(f"k + 1 = {k + 1} must fit one block of {self.block_size}")
+        self.k_cache, self.v_cache = k_cache, v_cache
+        self.q_len = q = k + 1
+        kv, d = k_cache.shape[2], k_cache.shape[3]
+        dev, dt = k_cache.device, k_cache.dtype
+        self.scale = scale
+        self.max_batch = max_batch
+        self.scratch_block = scratch_block
+        self.sizes = [b for b in VERIFY_SIZES if b < max_batch] + [max_batch]
+        width = -(-max_model_len // self.block_size)
+        self.q = torch.zeros(max_batch * q, num_heads, d, dtype=dt, device=dev)
+        self.k = torch.zeros(max_batch * q, kv, d, dtype=dt, device=dev)
+        self.v = torch.zeros(max_batch * q, kv, d, dtype=dt, device=dev)
+        self.pad_slots = scratch_block * self.block_size + torch.arange(q, dtype=torch.int64, device=dev)
+        self.slots = self.pad_slots.repeat(max_batch)
+        self.ctx = torch.full((max_batch,), q, dtype=torch.int32, device=dev)
+        self.tables = torch.full((max_batch, width), scratch_block, dtype=torch.int32, device=dev)
+        self.qstart = torch.arange(0, (max_batch + 1) * q, q, dtype=torch.int32, device=dev)
+        self.backend = AttentionBackend()
+        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata]] = {}
+
+    def _meta(self, b: int) -> AttnMetadata:
+        dev = self.k_cache.device
+        empty = torch.zeros(0, dtype=torch.int32, device=dev)
+        q = self.q_len
+        progs = (torch.arange(b, dtype=torch.int32, device=dev), torch.zeros(b, dtype=torch.int32, device=dev))
+        return AttnMetadata(
+            slot_mapping=self.slots[:b * q], num_prefill_tokens=b * q,
+            prefill_query_start=self.qstart[:b + 1], prefill_context_lens=self.ctx[:b],
+            prefill_block_tables=self.tables[:b],
+            decode_context_lens=empty, decode_block_tables=empty.view(0, 1), max_decode_context=0,
+            prefill_query_start_host=list(range(0, (b + 1) * q, q)), prefill_context_lens_host=[q] * b,
+            prefill_programs=progs,
+        )
+
+    def _forward(self, b: int, meta: AttnMetadata) -> torch.Tensor:
+        n = b * self.q_len
+        return self.backend.forward(self.q[:n], self.k[:n], self.v[:n], self.k_cache, self.v_cache, meta,
+                                    self.scale)
+
+    @torch.inference_mode()
+    def capture(self) -> None:
+        pool = torch.cuda.graph_pool_handle()
+        for b in reversed(self.sizes):
+            meta = self._meta(b)
+            for _ in range(2):
+                self._forward(b, meta)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                out = self._forward(b, meta)
+            self.graphs[b] = (g, out, meta)  # meta's tensors (the tile table) must outlive the graph
+        torch.cuda.synchronize()
+
+    def padded_size(self, n: int) -> int:
+        return self.sizes[bisect.bisect_left(self.sizes, n)]
+
+    @torch.inference_mode()
+    def load(self, q, k, v, slot_mapping, context_lens, block_tables) -> int:
+        """Copies one verification batch (n sequences, n * q tokens in sequence
+        order) into the static buffers and pads it; returns the captured size
+        that will run."""
+        qn = self.q_len
+        n = context_lens.shape[0]
+        if not 0 < n <= self.max_batch or q.shape[0] != n * qn:
+            raise ValueError(f"{n} sequences of {qn} tokens expected, got q {tuple(q.shape)}")
+        b = self.padded_size(n)
+        w = block_tables.shape[1]
+        if w > self.tables.shape[1]:
+            raise ValueError("block tables wider than max_model_len allows")
+        self.q[:n * qn].copy_(q)
+        self.k[:n * qn].copy_(k)
+        self.v[:n * qn].copy_(v)
+        self.slots[:n * qn].copy_(slot_mapping)
+        self.ctx[:n].copy_(context_lens)
+        self.tables[:n, :w].copy_(block_tables)
+        if b > n:
+            self.slots[n * qn:b * qn].copy_(self.pad_slots.repeat(b - n))
+            self.ctx[n:b].fill_(qn)
+            self.tables[n:b, 0].fill_(self.scratch_block)
+        return b
+
+    def replay(self, b: int) -> torch.Tensor:
+        g, out, _ = self.graphs[b]
+        g.replay()
+        return out
+
+    def run(self, q, k, v, slot_mapping, context_lens, block_tables) -> torch.Tensor:
+        """One verification step's attention: returns [n * q, H, D]."""
+        n = context_lens.shape[0]
+        return self.replay(self.load(q, k, v, slot_mapping, context_lens, block_tables))[:n * self.q_len]

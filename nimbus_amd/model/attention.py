@@ -62,8 +62,8 @@ class AttentionBackend:
     """
 
     def __init__(self, use_hip: bool = True, decode_workspace: torch.Tensor | None = None):
-        """decode_workspace (not in the reference): a zeroed decode workspace
-        (item counters + split partials, see paged_decode_attention) for this
+        """decode_workspace (not in the reference): a decode workspace (page
+        prefix sum + split partials, see paged_decode_attention) for this
         backend's decode calls instead of the per-stream cached one; a graph
         capture passes its own, sized for its largest batch."""
         if not use_hip:

@@ -1,5 +1,6 @@
-"""GPU: the drop-in backend (write -> prefill -> decode on one flat batch) and
-decode attention replayed from hipGraphs at padded batch sizes."""
+"""GPU: the drop-in backend (write -> prefill -> decode on one flat batch),
+decode attention replayed from hipGraphs at padded batch sizes, and
+speculative verification's prefill attention replayed from hipGraphs."""
 
 from __future__ import annotations
 
@@ -7,7 +8,7 @@ import pytest
 import torch
 
 from nimbus_amd import workloads
-from nimbus_amd.graphs import DecodeAttentionGraphs
+from nimbus_amd.graphs import DecodeAttentionGraphs, VerifyAttentionGraphs
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
 from tests.gpu_helpers import announce, oracle_decode, oracle_prefill
 from tests.helpers import assert_within
@@ -103,3 +104,46 @@ def test_decode_graph_replay_matches_eager(n):
     want = oracle_decode(da[0], kc_e, vc_e, ctx, da[4], b.scale)
     assert_within(eager.cpu(), want, what="eager vs oracle")
     assert_within(replays[0].cpu(), want, what="replay vs oracle")
+
+
+@pytest.mark.parametrize("n,q_len,dtype", [(3, 5, torch.bfloat16), (7, 5, torch.bfloat16), (16, 5, torch.bfloat16),
+                                           (5, 16, torch.float16)])
+def test_verify_graph_replay_matches_eager_and_oracle(n, q_len, dtype):
+    """Speculative verification (nimbus/spec/engine.py:60-150): n sequences of
+    q_len = k + 1 new tokens on cached contexts, captured once per padded size
+    with the precomputed tile table (arange(b), zeros(b)) and placeholder host
+    lists. Each replay, with eager work and synchronisations between
+    replays, is bit-identical to the eager backend call on the same
+    sequences (every prefill unit is independent of the tile order and of
+    the padding units), writes the same cache, and matches the oracle."""
+    announce(f"verify graph n={n} q_len={q_len} dtype={dtype}")
+    g = torch.Generator().manual_seed(n * 100 + q_len)
+    ctx = [int(c) for c in torch.randint(q_len + 1, 3000, (n,), generator=g)]
+    heads, kv, d = (32, 8, 128) if dtype == torch.bfloat16 else (32, 4, 64)
+    b = workloads.build_batch([(c, q_len) for c in ctx], heads=heads, kv_heads=kv, head_dim=d, dtype=dtype,
+                              device="cuda", seed=n, pool_factor=1.3, write_first=False)
+    nb = b.k_cache.shape[0]
+    kc = torch.cat([b.k_cache, torch.zeros_like(b.k_cache[:1])])  # + the scratch block
+    vc = torch.cat([b.v_cache, torch.zeros_like(b.v_cache[:1])])
+    graphs = VerifyAttentionGraphs(kc, vc, num_heads=heads, scale=b.scale, max_model_len=4096, max_batch=16,
+                                   k=q_len - 1, scratch_block=nb)
+    graphs.capture()
+    pa = b.prefill_args()
+    empty = torch.zeros(0, dtype=torch.int32, device="cuda")
+    meta = AttnMetadata(
+        slot_mapping=b.slot_mapping, num_prefill_tokens=n * q_len, prefill_query_start=pa[3],
+        prefill_context_lens=pa[4], prefill_block_tables=b.block_tables, decode_context_lens=empty,
+        decode_block_tables=empty.view(0, 1), max_decode_context=0, prefill_query_start_host=pa[7],
+        prefill_context_lens_host=pa[8])
+    kc_e, vc_e = kc.clone(), vc.clone()
+    eager = AttentionBackend().forward(b.q, b.k, b.v, kc_e, vc_e, meta, b.scale)
+    replays = []
+    for rep in range(3):
+        replays.append(graphs.run(b.q, b.k, b.v, b.slot_mapping, pa[4], b.block_tables).clone())
+        torch.cuda.synchronize()
+        _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # eager work between replays
+    for rep, got in enumerate(replays):
+        assert torch.equal(got, eager), f"replay {rep} differs from the eager call"
+    assert torch.equal(kc[:nb], kc_e[:nb]) and torch.equal(vc[:nb], vc_e[:nb])
+    want = oracle_prefill(b.q, kc_e, vc_e, pa[7], pa[8], b.block_tables, b.scale)
+    assert_within(replays[0].cpu(), want, what="verify replay vs oracle")
