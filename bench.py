@@ -295,10 +295,12 @@ def time_mixed_step(batch, steps, warmup):
 def time_verify(steps, warmup, n=16, k=4):
     """Speculative verification's attention (nimbus/spec/engine.py:60-150):
     n sequences of k + 1 new tokens on Llama-3-8B-shaped contexts (log-uniform
-    128..8192), slot write + prefill replayed from a hipGraph. Bytes: every
-    visible K/V row once per kv head, the new tokens' K/V written and q/out.
-    The paged decode call on the same contexts (one token each) is timed
-    beside it as the bandwidth reference."""
+    128..8192), slot write + prefill replayed from a hipGraph, once as the
+    prefill call routes it (its verify form) and once pinned to the tile
+    kernel (the reference's route). Bytes: every visible K/V row once per kv
+    head, the new tokens' K/V written and q/out. The paged decode call on the
+    same contexts (one token each) is timed beside it as the bandwidth
+    reference."""
     import torch
 
     from nimbus_amd import workloads
@@ -313,14 +315,19 @@ def time_verify(steps, warmup, n=16, k=4):
     nb = b.k_cache.shape[0]
     kc = torch.cat([b.k_cache, torch.zeros_like(b.k_cache[:1])])
     vc = torch.cat([b.v_cache, torch.zeros_like(b.v_cache[:1])])
-    graphs = VerifyAttentionGraphs(kc, vc, num_heads=32, scale=b.scale, max_model_len=8192, max_batch=n, k=k,
-                                   scratch_block=nb)
-    graphs.capture()
     pa = b.prefill_args()
-    gb = graphs.load(b.q, b.k, b.v, b.slot_mapping, pa[4], b.block_tables)
-    for _ in range(warmup):
-        graphs.replay(gb)
-    us = statistics.mean(event_times_us(lambda i: graphs.replay(gb), steps, torch.cuda.current_stream()))
+    times = {}
+    for kernel in ("auto", "tile"):
+        graphs = VerifyAttentionGraphs(kc, vc, num_heads=32, scale=b.scale, max_model_len=8192, max_batch=n, k=k,
+                                       scratch_block=nb, kernel=kernel)
+        graphs.capture()
+        gb = graphs.load(b.q, b.k, b.v, b.slot_mapping, pa[4], b.block_tables)
+        for _ in range(warmup):
+            graphs.replay(gb)
+        times[kernel] = statistics.mean(event_times_us(lambda i: graphs.replay(gb), steps,
+                                                       torch.cuda.current_stream()))
+        del graphs
+    us = times["auto"]
     kv_bytes = sum(ctx) * 2 * 8 * 128 * 2
     nbytes = kv_bytes + 2 * n * q_len * 32 * 128 * 2 + 2 * n * q_len * 8 * 128 * 2 * 2
     # the decode kernel over the same contexts
@@ -334,7 +341,7 @@ def time_verify(steps, warmup, n=16, k=4):
                                          workspace=ws), steps, torch.cuda.current_stream()))
     return {"workload": f"{n} sequences x {q_len} tokens (k={k}), Llama-3-8B shape, contexts log-uniform "
                         f"[128, 8192] (sum {sum(ctx)})", "us_per_replay": us, "bytes": nbytes,
-            "GBps": nbytes / us / 1e3, "decode_same_contexts_us": dus,
+            "GBps": nbytes / us / 1e3, "tile_kernel_us_per_replay": times["tile"], "decode_same_contexts_us": dus,
             "decode_same_contexts_GBps": (kv_bytes + 2 * n * 32 * 128 * 2) / dus / 1e3}
 
 

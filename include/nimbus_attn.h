@@ -2,8 +2,10 @@
  * nimbus_attn.h - C ABI of the MI355X (gfx950) paged-attention library.
  *
  * libnimbus_attn.so replaces the GPU side of Nimbus's attention hot path:
- * the KV slot write, paged decode attention and causal varlen paged prefill
- * attention, and the fused residual add + RMSNorm on either side of it. Every entry point takes plain device pointers, element strides
+ * the KV slot write, paged decode attention, causal varlen paged prefill
+ * attention (with a verify form for uniform short query runs), and the
+ * fused residual add + RMSNorm on either side of it. Every entry point
+ * takes plain device pointers, element strides
  * (not bytes), sizes, a dtype code and an opaque hipStream_t; none allocates,
  * frees, synchronises or reads device memory on the host, so each call can be
  * recorded into a hipGraph. PyTorch (or any caller) owns every buffer.
@@ -25,7 +27,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 3
+#define NIMBUS_ATTN_ABI_VERSION 4
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -143,6 +145,40 @@ int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, 
                          int32_t num_programs, void* out, int64_t out_stride_t, int64_t out_stride_h,
                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
                          int32_t dtype, void* stream);
+
+/*
+ * Bytes of workspace nimbus_paged_verify needs (as for the decode workspace,
+ * with queries_per_seq columns per head). -1 for queries_per_seq outside
+ * [1, 16].
+ */
+int64_t nimbus_paged_verify_workspace_bytes(int32_t batch, int32_t queries_per_seq, int32_t num_heads,
+                                            int32_t head_dim, int64_t max_context);
+
+/*
+ * Speculative-verify attention: causal attention of each sequence's newest
+ * queries_per_seq tokens over its paged cache, when every sequence has the
+ * same number (1..16) of new tokens. Computes what nimbus_paged_prefill
+ * computes for query_start = arange(batch + 1) * queries_per_seq (the
+ * verification batch of nimbus/spec/engine.py:84-96, which runs
+ * nimbus/kernels/prefill_attention.py:93-119 at q_len = k + 1), with the
+ * page-split decode kernels: the queries of a sequence are extra MFMA
+ * columns, so each K/V page is read once for all of them.
+ *
+ * q/out hold batch * queries_per_seq token rows in sequence order: row
+ * b * queries_per_seq + j is query j of sequence b, which sits at position
+ * context_lens[b] - queries_per_seq + j and sees keys up to it (a query
+ * that sees no key, when context_lens[b] < queries_per_seq, gives 0). The
+ * _b strides are per token row. Every other argument, the workspace rule
+ * (sized by nimbus_paged_verify_workspace_bytes) and the grid rule are
+ * nimbus_paged_decode's; queries_per_seq = 1 is nimbus_paged_decode.
+ */
+int nimbus_paged_verify(int32_t queries_per_seq, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                        const void* k_cache, const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                        int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                        int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
+                        int64_t out_stride_b, int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
+                        int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        int32_t block_size, int64_t max_context, float scale, int32_t dtype, void* stream);
 
 /*
  * Fused residual add + RMSNorm. Replaces nimbus/kernels/rmsnorm.py:21-59

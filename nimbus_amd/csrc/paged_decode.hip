@@ -3,6 +3,13 @@
 // Replaces nimbus/kernels/paged_attention.py:25-146 (the Triton
 // _paged_decode_kernel, _merge_partitions_kernel and their wrapper).
 //
+// The same kernels serve speculative verification (nimbus_paged_verify):
+// every sequence then has nq query tokens, its newest nq positions, and
+// query j sees keys 0 .. ctx - nq + j (the causal rule of
+// nimbus/kernels/prefill_attention.py:27-78 for q_len = nq). The nq queries
+// of a sequence become extra MFMA columns ("virtual heads": column = query j,
+// head g), so each K/V page is read once for all of them.
+//
 // Work split (stream-K over the batch's pages). The 16-token pages of all
 // sequences are laid end to end. For each kv-head group (a kv head and up to
 // 16 of the query heads that share it, so each K/V page is read from HBM
@@ -18,7 +25,7 @@
 // of K/V in flight in a ring of register buffers (page x + kRing is issued
 // as soon as page x has been consumed), and finds each page's id kRing + 2
 // pages ahead with scalar loads that never wait behind the vector loads.
-// Per page, with G query heads padded to 16 MFMA columns:
+// Per page, with the nq x G (query, head) columns padded to 16 per chunk:
 //   S^T[token][g] = K[token][:] . Q^T[:][g]   (16x16x32 MFMA, K straight from
 //                                               HBM into the A-operand layout)
 //   online softmax per column g in fp32 (exp2 domain), reductions across the
@@ -50,6 +57,11 @@ constexpr int kMinPagesPerWave = 8;   // slices shorter than this only add merge
 constexpr int kMaxDecodeBatch = 4096; // LDS holds the batch's page prefix sum
 constexpr int kWavesPerCU = 8;        // two waves of the page kernel per SIMD
 constexpr int kRing = 3;              // pages of K/V in flight per wave
+constexpr int kMaxVerifyQueries = 16; // queries per sequence of a verify call
+// Running-max floor: finite, below any score, so a column that sees no key
+// in a piece (a verify query whose causal limit ends before the piece) keeps
+// exp2(m - m) = 1 and weights exp2(-inf - m) = 0 instead of NaN.
+constexpr float kNoScore = -1e30f;
 // gfx950 parts have 256 CUs; launches never exceed this many resident waves,
 // which keeps the workspace size a pure function of the call's shape.
 constexpr int64_t kMaxResidentWaves = 256 * kWavesPerCU;
@@ -68,9 +80,11 @@ struct DecodeArgs {
   uint16_t* out;
   int64_t o_sb, o_sh;
   int32_t* pre_out;  // workspace: the page prefix sum [B + 1], for the merge pass
-  float* part_ml;    // workspace: [slot][H][2] (m, l) of partial pieces
-  float* part_o;     // workspace: [slot][H][D] unnormalised O of partial pieces
+  float* part_ml;    // workspace: [slot][nq * H][2] (m, l) of partial pieces
+  float* part_o;     // workspace: [slot][nq * H][D] unnormalised O of partial pieces
   int32_t B, H, G, gchunks, kvg;
+  int32_t nkv;       // kv heads
+  int32_t nq;        // query tokens per sequence (1 for decode)
   int32_t nwk;       // waves launched per kv-head group
   int32_t max_ctx;   // context bound: min(max_context, block-table width * 16)
   float scale_log2;
@@ -170,10 +184,17 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
   const int grp = lane / 16;
   const int kg = blockIdx.x % a.kvg;
   const int idx = blockIdx.x / a.kvg;
-  const int kvh = kg / a.gchunks;
-  const int g0 = (kg % a.gchunks) * 16;
-  const bool g_ok = g0 + col < a.G;
-  const int head = kvh * a.G + (g_ok ? g0 + col : 0);
+  // Chunk-major: the column chunks of one kv head sit a.nkv blocks apart,
+  // on one XCD when a.nkv is a multiple of 8, so a page the first chunk's
+  // wave fetches is in that XCD's L2 for the second.
+  const int kvh = kg % a.nkv;
+  const int g0 = (kg / a.nkv) * 16;
+  const int vcol = g0 + col;  // virtual column: query vcol / G, head vcol % G
+  const bool g_ok = vcol < a.nq * a.G;
+  const int qj = g_ok ? vcol / a.G : 0;
+  const int head = kvh * a.G + (g_ok ? vcol - qj * a.G : 0);
+  const int back = a.nq - 1 - qj;  // keys this query sees fewer than the newest
+  const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;  // partial-piece row
 
   page_prefix(a, pre);
   const int total = __builtin_amdgcn_readfirstlane(pre[a.B]);
@@ -190,10 +211,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
   const uint16_t* vbase = a.vc + static_cast<int64_t>(kvh) * a.c_sh;
 
   // Q^T as the B operand: column g, k-group grp holds q[g][32kk + 8grp .. +8].
-  // Columns past G read head kvh * G (a valid row) and are never written, so
-  // the load needs no mask and nothing waits for it before its first use.
+  // Columns past nq x G read query 0, head kvh * G (a valid row) and are
+  // never written, so the load needs no mask and nothing waits for it before
+  // its first use.
   auto load_q = [&](int b, u32x4* dst) {
-    const uint16_t* qrow = a.q + b * a.q_sb + static_cast<int64_t>(head) * a.q_sh;
+    const int64_t tok = static_cast<int64_t>(b) * a.nq + qj;
+    const uint16_t* qrow = a.q + tok * a.q_sb + static_cast<int64_t>(head) * a.q_sh;
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) dst[kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * grp);
   };
@@ -267,7 +290,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
   const int tr_chunk = (col % 4) / 2;
 
   int seg0 = lo;  // first flat page of the current piece
-  float m_run = -INFINITY;
+  float m_run = kNoScore;
   float l_run = 0.f;
   f32x4 acc[NN];
 #pragma unroll
@@ -279,7 +302,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     const bool more = x + 1 < hi;
     const bool piece_ends = !more || ref[1].b != cur.b;
     ref[kRing + 1] = locate(x + kRing + 1);  // scalar loads, used two steps from now
-    const int valid = min(kPage, min(cur.ctx_raw, a.max_ctx) - kPage * cur.p);  // >= 1
+    const int ctx_left = min(cur.ctx_raw, a.max_ctx) - kPage * cur.p;  // >= 1
+    const int valid = min(kPage, ctx_left);
 
     // Stage V as loaded. Rows past the context (only on a sequence's last
     // page) are zeroed: P is 0 there, but 0 * garbage must not reach the sum.
@@ -301,10 +325,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     if (x + kRing < hi) load_page(bf, ref[kRing]);
     if (piece_ends && more) load_q(ref[1].b, qnext);
 
+    // Causal limit of this column's query: rows below ctx_left - back.
+    const int lim = ctx_left - back;
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float xs = 4 * grp + r < valid ? s[r] * a.scale_log2 : -INFINITY;
+      const float xs = 4 * grp + r < lim ? s[r] * a.scale_log2 : -INFINITY;
       s[r] = xs;
       mx = fmaxf(mx, xs);
     }
@@ -360,8 +386,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
       const bool whole = seg0 == pre[rb] && x + 1 == pre[rb + 1];
       if (g_ok) {
         if (whole) {
-          const float inv = 1.f / l;
-          uint16_t* orow = a.out + rb * a.o_sb + static_cast<int64_t>(head) * a.o_sh;
+          const float inv = l > 0.f ? 1.f / l : 0.f;  // a query that sees no key gives 0
+          const int64_t tok = static_cast<int64_t>(rb) * a.nq + qj;
+          uint16_t* orow = a.out + tok * a.o_sb + static_cast<int64_t>(head) * a.o_sh;
 #pragma unroll
           for (int nn = 0; nn < NN; ++nn) {
             const f32x4 o = acc[nn];
@@ -370,14 +397,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
             *reinterpret_cast<u32x2*>(orow + 16 * nn + 4 * grp) = w;
           }
         } else {
-          const int64_t row = (static_cast<int64_t>(idx) + rb) * a.H + head;
+          const int64_t row = (static_cast<int64_t>(idx) + rb) * a.nq * a.H + vhead;
           float* po = a.part_o + row * D;
 #pragma unroll
           for (int nn = 0; nn < NN; ++nn) *reinterpret_cast<f32x4*>(po + 16 * nn + 4 * grp) = acc[nn];
           if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run, l);
         }
       }
-      m_run = -INFINITY;
+      m_run = kNoScore;
       l_run = 0.f;
 #pragma unroll
       for (int nn = 0; nn < NN; ++nn) acc[nn] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -401,9 +428,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
 // Second pass: for every sequence whose pages were split between waves,
 // o = sum_i O_i w_i / sum_i L_i w_i with w_i = 2^(m_i - max m) over its
 // pieces (nimbus/kernels/paged_attention.py:83-98), in one pass with a
-// running max. One wave per (sequence, kv-head group): lane = (head of the
-// group, 8 consecutive elements of d); sequences held whole by one wave exit
-// at once.
+// running max. One wave per (sequence, kv-head group): lane = (column of
+// the group, 8 consecutive elements of d); sequences held whole by one wave
+// exit at once.
 template <int DT, int D>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int SEG = D / 8;  // lanes per head
@@ -417,18 +444,21 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   const int i0 = slice_owner(first, nw, total);
   const int i1 = slice_owner(last, nw, total);
   if (i0 == i1) return;
-  const int kvh = kg / a.gchunks;
-  const int g0 = (kg % a.gchunks) * 16;
-  const int gcount = min(16, a.G - g0);
+  const int kvh = kg % a.nkv;
+  const int g0 = (kg / a.nkv) * 16;
+  const int gcount = min(16, a.nq * a.G - g0);
   for (int e = threadIdx.x; e < gcount * SEG; e += 64) {
-    const int head = kvh * a.G + g0 + e / SEG;
+    const int vcol = g0 + e / SEG;
+    const int qj = vcol / a.G;
+    const int head = kvh * a.G + vcol - qj * a.G;
+    const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;
     const int d0 = 8 * (e % SEG);
     float M = -INFINITY, L = 0.f;
     float O[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) O[k] = 0.f;
     for (int i = i0; i <= i1; ++i) {
-      const int64_t row = (static_cast<int64_t>(i) + b) * a.H + head;
+      const int64_t row = (static_cast<int64_t>(i) + b) * a.nq * a.H + vhead;
       const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
       const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
       const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
@@ -443,8 +473,9 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
         O[k + 4] = O[k + 4] * wo + o1[k] * wi;
       }
     }
-    const float inv = 1.f / L;
-    uint16_t* orow = a.out + b * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    const int64_t tok = static_cast<int64_t>(b) * a.nq + qj;
+    uint16_t* orow = a.out + tok * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
     const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O[0] * inv), Elem<DT>::from_f32(O[1] * inv)),
                           pack2(Elem<DT>::from_f32(O[2] * inv), Elem<DT>::from_f32(O[3] * inv)),
                           pack2(Elem<DT>::from_f32(O[4] * inv), Elem<DT>::from_f32(O[5] * inv)),
@@ -488,8 +519,8 @@ static int launch_decode(const DecodeArgs& a, int phases, hipStream_t stream) {
 using namespace nimbus;
 
 // Workspace layout, each part 256-byte aligned: page prefix [B + 1] int32;
-// per slot (wave index + sequence, < waves per kv group + B) and query head
-// the (m, l) pair; per slot and head D floats of O.
+// per slot (wave index + sequence, < waves per kv group + B) and (query,
+// head) column the (m, l) pair; per slot and column D floats of O.
 static int64_t round256(int64_t n) { return (n + 255) / 256 * 256; }
 static int64_t prefix_bytes(int64_t batch) { return round256((batch + 1) * 4); }
 
@@ -497,15 +528,28 @@ static int64_t max_pages_of(int64_t batch, int64_t max_context) {
   return batch * ((max_context + kPage - 1) / kPage);
 }
 
-extern "C" int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
-                                                       int64_t max_context) {
-  if (batch < 0 || num_heads <= 0 || head_dim <= 0 || max_context < 0) return -1;
+static int64_t workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim, int64_t max_context,
+                              int32_t nq) {
+  if (batch < 0 || num_heads <= 0 || head_dim <= 0 || max_context < 0 || nq <= 0) return -1;
   // Any device and any kvg >= 1 launch at most this many waves per kv group.
   const int64_t slots = waves_per_group(kMaxResidentWaves, 1, max_pages_of(batch, max_context)) + batch;
-  return prefix_bytes(batch) + round256(slots * num_heads * 2 * 4) + slots * num_heads * head_dim * 4;
+  const int64_t cols = static_cast<int64_t>(num_heads) * nq;
+  return prefix_bytes(batch) + round256(slots * cols * 2 * 4) + slots * cols * head_dim * 4;
 }
 
-static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+extern "C" int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
+                                                       int64_t max_context) {
+  return workspace_size(batch, num_heads, head_dim, max_context, 1);
+}
+
+extern "C" int64_t nimbus_paged_verify_workspace_bytes(int32_t batch, int32_t queries_per_seq, int32_t num_heads,
+                                                       int32_t head_dim, int64_t max_context) {
+  if (queries_per_seq > kMaxVerifyQueries) return -1;
+  return workspace_size(batch, num_heads, head_dim, max_context, queries_per_seq);
+}
+
+static int paged_decode_impl(int phases, int32_t nq, const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                             const void* k_cache,
                              const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
                              int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
                              int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
@@ -513,6 +557,8 @@ static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int6
                              int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                              int32_t block_size, int64_t max_context, float scale, int32_t dtype, void* stream) {
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return NIMBUS_ERR_INVALID;
+  if (nq <= 0) return NIMBUS_ERR_INVALID;
+  if (nq > kMaxVerifyQueries) return NIMBUS_ERR_UNSUPPORTED;
   if (block_size != kPage) return NIMBUS_ERR_UNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return NIMBUS_ERR_UNSUPPORTED;
   if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
@@ -528,7 +574,7 @@ static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int6
        reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(out) |
        reinterpret_cast<uintptr_t>(workspace)) % 16 != 0)
     return NIMBUS_ERR_ALIGNMENT;
-  const int64_t need = nimbus_paged_decode_workspace_bytes(batch, num_heads, head_dim, max_context);
+  const int64_t need = workspace_size(batch, num_heads, head_dim, max_context, nq);
   if (need < 0) return NIMBUS_ERR_INVALID;
   if (workspace == nullptr || workspace_bytes < need) return NIMBUS_ERR_WORKSPACE;
   int64_t cus = 0;
@@ -555,7 +601,9 @@ static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int6
   a.B = batch;
   a.H = num_heads;
   a.G = num_heads / num_kv_heads;
-  a.gchunks = (a.G + 15) / 16;
+  a.nq = nq;
+  a.nkv = num_kv_heads;
+  a.gchunks = (nq * a.G + 15) / 16;
   a.kvg = num_kv_heads * a.gchunks;
   const int64_t ctx_bound = max_context < static_cast<int64_t>(bt_width) * kPage
                                 ? max_context
@@ -569,7 +617,8 @@ static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int6
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   a.pre_out = reinterpret_cast<int32_t*>(ws);
   a.part_ml = reinterpret_cast<float*>(ws + prefix_bytes(batch));
-  a.part_o = reinterpret_cast<float*>(ws + prefix_bytes(batch) + round256(slots * num_heads * 2 * 4));
+  const int64_t cols = static_cast<int64_t>(num_heads) * nq;
+  a.part_o = reinterpret_cast<float*>(ws + prefix_bytes(batch) + round256(slots * cols * 2 * 4));
   a.scale_log2 = scale * 1.4426950408889634f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -592,10 +641,19 @@ static int paged_decode_impl(int phases, const void* q, int64_t q_stride_b, int6
       workspace, workspace_bytes, batch, num_heads, num_kv_heads, head_dim, block_size, max_context, scale, \
       dtype, stream
 
-extern "C" int nimbus_paged_decode(NIMBUS_DECODE_PARAMS) { return paged_decode_impl(3, NIMBUS_DECODE_ARGS); }
+extern "C" int nimbus_paged_decode(NIMBUS_DECODE_PARAMS) { return paged_decode_impl(3, 1, NIMBUS_DECODE_ARGS); }
 
 extern "C" int nimbus_paged_decode_pages(NIMBUS_DECODE_PARAMS) {
-  return paged_decode_impl(1, NIMBUS_DECODE_ARGS);
+  return paged_decode_impl(1, 1, NIMBUS_DECODE_ARGS);
 }
 
-extern "C" int nimbus_paged_decode_merge(NIMBUS_DECODE_PARAMS) { return paged_decode_impl(2, NIMBUS_DECODE_ARGS); }
+extern "C" int nimbus_paged_decode_merge(NIMBUS_DECODE_PARAMS) {
+  return paged_decode_impl(2, 1, NIMBUS_DECODE_ARGS);
+}
+
+// q and out hold batch * queries_per_seq tokens in sequence order (token
+// b * queries_per_seq + j is query j of sequence b); the stride arguments
+// named _b are per token.
+extern "C" int nimbus_paged_verify(int32_t queries_per_seq, NIMBUS_DECODE_PARAMS) {
+  return paged_decode_impl(3, queries_per_seq, NIMBUS_DECODE_ARGS);
+}

@@ -18,7 +18,8 @@ device memory on the host or issues a memset.
 
 VerifyAttentionGraphs does the same for speculative verification
 (nimbus/spec/engine.py:60-150): there every sequence feeds k + 1 tokens, all
-through the prefill kernel.
+through the prefill call, which runs them in its verify form (the page-split
+decode kernels with k + 1 query columns per head) when they fit it.
 """
 
 from __future__ import annotations
@@ -27,7 +28,9 @@ import bisect
 
 import torch
 
-from nimbus_amd.kernels.paged_attention import decode_workspace_bytes, new_decode_workspace
+from nimbus_amd.kernels.paged_attention import (PAGE, decode_workspace_bytes, new_decode_workspace,
+                                                verify_workspace_bytes)
+from nimbus_amd.kernels.prefill_attention import verify_queries
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
 
 PADDED_SIZES = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128)
@@ -144,10 +147,16 @@ class VerifyAttentionGraphs:
     - padding sequences (up to the captured sizes 1, 2, 4, 8, 16 below
       max_batch, then max_batch) have context q and write and read the
       scratch block, which holds q <= block_size tokens (:118-126).
+
+    kernel: "auto" lets the prefill call pick its verify form (a workspace
+    for it, sized for max_batch and max_model_len, is owned here); "tile"
+    pins the tile kernel, as in the reference.
     """
 
     def __init__(self, k_cache: torch.Tensor, v_cache: torch.Tensor, num_heads: int, scale: float,
-                 max_model_len: int, max_batch: int, k: int, scratch_block: int):
+                 max_model_len: int, max_batch: int, k: int, scratch_block: int, kernel: str = "auto"):
+        if kernel not in ("auto", "tile"):
+            raise ValueError(f"kernel must be 'auto' or 'tile', got {kernel!r}")
         self.block_size = k_cache.shape[1]
         if not 0 < k + 1 <= self.block_size:
             raise ValueError(f"k + 1 = {k + 1} must fit one block of {self.block_size}")
@@ -168,7 +177,13 @@ class VerifyAttentionGraphs:
         self.ctx = torch.full((max_batch,), q, dtype=torch.int32, device=dev)
         self.tables = torch.full((max_batch, width), scratch_block, dtype=torch.int32, device=dev)
         self.qstart = torch.arange(0, (max_batch + 1) * q, q, dtype=torch.int32, device=dev)
-        self.backend = AttentionBackend()
+        self.kernel = kernel
+        workspace = None
+        if kernel == "auto" and verify_queries(list(range(0, (max_batch + 1) * q, q)), num_heads, kv):
+            # the verify form bounds contexts by the block-table width
+            nbytes = verify_workspace_bytes(max_batch, q, num_heads, d, width * PAGE)
+            workspace = new_decode_workspace(nbytes, dev)
+        self.backend = AttentionBackend(decode_workspace=workspace)
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata]] = {}
 
     def _meta(self, b: int) -> AttnMetadata:
@@ -182,7 +197,7 @@ class VerifyAttentionGraphs:
             prefill_block_tables=self.tables[:b],
             decode_context_lens=empty, decode_block_tables=empty.view(0, 1), max_decode_context=0,
             prefill_query_start_host=list(range(0, (b + 1) * q, q)), prefill_context_lens_host=[q] * b,
-            prefill_programs=progs,
+            prefill_programs=progs, prefill_kernel=None if self.kernel == "auto" else self.kernel,
         )
 
     def _forward(self, b: int, meta: AttnMetadata) -> torch.Tensor:

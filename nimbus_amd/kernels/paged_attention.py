@@ -134,3 +134,79 @@ def paged_decode_attention(
         _lib.dtype_code(q.dtype), _lib.stream_of(q))
     _lib.check(rc, _entry)
     return out
+
+
+MAX_VERIFY_QUERIES = 16  # queries per sequence nimbus_paged_verify takes
+
+
+def verify_workspace_bytes(batch: int, queries_per_seq: int, heads: int, head_dim: int, max_context: int) -> int:
+    return int(_lib.load().nimbus_paged_verify_workspace_bytes(batch, queries_per_seq, heads, head_dim,
+                                                                max_context))
+
+
+def paged_verify_attention(
+    q: torch.Tensor,  # [B * nq, H, D], sequence b's queries in rows b * nq .. b * nq + nq - 1
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    context_lens: torch.Tensor,  # [B] int32, including the nq new tokens
+    block_tables: torch.Tensor,  # [B, max_blocks] int32
+    queries_per_seq: int,
+    max_context: int,
+    scale: float,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Causal attention of each sequence's newest queries_per_seq tokens over
+    its paged cache (nimbus_paged_verify): what paged_prefill_attention
+    computes for query_start = arange(B + 1) * queries_per_seq, with the
+    page-split decode kernels reading each K/V page once for all the queries.
+
+    Query j of sequence b sits at position context_lens[b] - nq + j and sees
+    keys up to it. max_context bounds every context length, as for decode;
+    the launch grid depends on it and on the shapes only. `workspace`: as
+    for paged_decode_attention, at least verify_workspace_bytes().
+    """
+    nq = int(queries_per_seq)
+    if q.dim() != 3:
+        raise ValueError(f"q must be [B * nq, H, D], got {tuple(q.shape)}")
+    t, h, d = q.shape
+    _check_cache(k_cache, v_cache)
+    kv = k_cache.shape[2]
+    if k_cache.shape[3] != d or h % kv != 0:
+        raise ValueError(f"q {tuple(q.shape)} does not fit caches {tuple(k_cache.shape)}")
+    if q.dtype != k_cache.dtype:
+        raise ValueError("q and the caches must share one dtype")
+    if not 1 <= nq <= MAX_VERIFY_QUERIES:
+        raise ValueError(f"queries_per_seq must be in 1..{MAX_VERIFY_QUERIES}, got {nq}")
+    if context_lens.dtype != torch.int32 or block_tables.dtype != torch.int32:
+        raise ValueError("context_lens and block_tables must be int32")
+    b = context_lens.shape[0]
+    if context_lens.dim() != 1 or t != b * nq or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise ValueError(f"q must hold {nq} rows per sequence of context_lens [B], block_tables [B, max_blocks]")
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise ValueError("out must match q's shape and dtype with unit last stride")
+    if b == 0:
+        return out
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    context_lens = context_lens.contiguous()
+    if block_tables.stride(1) != 1:
+        block_tables = block_tables.contiguous()
+    lib = _lib.load()
+    need = lib.nimbus_paged_verify_workspace_bytes(b, nq, h, d, int(max_context))
+    if workspace is not None:
+        if workspace.numel() * workspace.element_size() < need or not workspace.is_cuda:
+            raise ValueError(f"workspace smaller than the {need} bytes this call needs")
+        ws = workspace
+    else:
+        ws = _cached_workspace(need, q.device)
+    rc = lib.nimbus_paged_verify(
+        nq, q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(), block_tables.stride(0),
+        block_tables.shape[1], context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), ws.numel() * ws.element_size(), b, h, kv, d, k_cache.shape[1], int(max_context), float(scale),
+        _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, "nimbus_paged_verify")
+    return out

@@ -6,6 +6,12 @@ csrc/paged_prefill.hip. A sequence's queries are its newest q_len tokens;
 query j sits at absolute position ctx - q_len + j. This covers fresh prompts
 (q_len == ctx), chunked prefill over a cached prefix and speculative
 verification of several draft tokens.
+
+A batch in which every sequence has the same short q_len (speculative
+verification: k + 1 tokens each, nimbus/spec/engine.py:84-96) runs instead
+on the page-split decode kernels through nimbus_paged_verify, which read
+each K/V page once for all of a sequence's queries; the tile kernel would
+spend a 64-row tile on a handful of queries.
 """
 
 from __future__ import annotations
@@ -14,12 +20,33 @@ import numpy as np
 import torch
 
 from nimbus_amd import _lib
-from nimbus_amd.kernels.paged_attention import _check_cache
+from nimbus_amd.kernels.paged_attention import MAX_VERIFY_QUERIES, PAGE, _check_cache, paged_verify_attention
 
 BLOCK_M = 64  # query positions per tile-table entry (NIMBUS_PREFILL_TILE)
 # Tiles whose workgroups all fit the chip at once: a GQA tile is typically 16
 # workgroups (kv-head groups x sub-tiles), and 256 CUs hold two each.
 PAIRED_TILES = 32
+# The verify form takes a batch while a sequence's queries times the heads of
+# a kv group fit this many MFMA columns: each 16 columns more read every K/V
+# page once more.
+VERIFY_MAX_COLUMNS = 32
+MAX_VERIFY_SEQUENCES = 4096  # the decode kernels' batch limit
+
+
+def verify_queries(query_start_host: list[int], num_heads: int, num_kv_heads: int) -> int:
+    """q_len if every sequence of the batch has the same q_len and the verify
+    form takes it (see VERIFY_MAX_COLUMNS), else 0."""
+    n = len(query_start_host) - 1
+    if not 1 <= n <= MAX_VERIFY_SEQUENCES or query_start_host[0] != 0:
+        return 0
+    nq = query_start_host[1]
+    if not 1 <= nq <= MAX_VERIFY_QUERIES or query_start_host[-1] != n * nq:
+        return 0
+    if nq * (num_heads // num_kv_heads) > VERIFY_MAX_COLUMNS:
+        return 0
+    if n > 1 and not np.all(np.diff(np.asarray(query_start_host, dtype=np.int64)) == nq):
+        return 0
+    return nq
 
 
 def build_programs(query_start_host: list[int], device,
@@ -74,14 +101,25 @@ def paged_prefill_attention(
     context_lens_host: list[int],
     programs: tuple[torch.Tensor, torch.Tensor] | None = None,
     out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    kernel: str = "auto",
 ) -> torch.Tensor:
     """Causal attention of each sequence's newest tokens over its paged cache.
 
     The cache must already hold the new tokens' K/V (write_kv runs first, as
     in nimbus/model/attention.py:78). `programs` is build_programs' tile table
-    (built here when None). `out` (optional, not in the reference signature)
-    receives the result in place.
+    (built here when None). Not in the reference signature: `out` receives
+    the result in place; `kernel` is "auto" (the verify form when
+    verify_queries() takes the batch, else the tile kernel), "tile" or
+    "verify"; `workspace` is the verify form's (paged_verify_attention), by
+    default the per-stream cached one.
+
+    The verify form bounds context lengths by the block-table width (16
+    tokens a column), not by context_lens_host: Nimbus's verify graphs pass
+    placeholder host context lengths (spec/engine.py:94).
     """
+    if kernel not in ("auto", "tile", "verify"):
+        raise ValueError(f"kernel must be 'auto', 'tile' or 'verify', got {kernel!r}")
     if q.dim() != 3:
         raise ValueError(f"q must be [Tp, H, D], got {tuple(q.shape)}")
     t, h, d = q.shape
@@ -102,6 +140,13 @@ def paged_prefill_attention(
             raise ValueError(f"{name} must be int32")
     if block_tables.dim() != 2 or block_tables.shape[0] != len(query_start_host) - 1:
         raise ValueError("block_tables must be [P, max_blocks]")
+    nq = verify_queries(query_start_host, h, kv) if kernel != "tile" else 0
+    if kernel == "verify" and nq == 0:
+        raise ValueError("the verify form needs 1..16 queries in every sequence, fitting "
+                         f"{VERIFY_MAX_COLUMNS} columns per kv group")
+    if nq:
+        return paged_verify_attention(q, k_cache, v_cache, context_lens, block_tables, nq,
+                                      block_tables.shape[1] * PAGE, scale, out=out, workspace=workspace)
     if programs is None:
         programs = build_programs(query_start_host, q.device, context_lens_host)
     prog_seq, prog_m = programs

@@ -42,6 +42,10 @@ class AttnMetadata:
     # Fixed decode launch grid of the reference's graph capture (accepted, unused:
     # the grid here is pinned by max_decode_context)
     decode_partitions: int | None = None
+    # Not in the reference: which prefill kernel serves this step ("tile" or
+    # "verify", see prefill_attention.verify_queries), decided once per step
+    # by the backend like the tile table.
+    prefill_kernel: str | None = None
 
     @property
     def num_prefills(self) -> int:
@@ -62,10 +66,10 @@ class AttentionBackend:
     """
 
     def __init__(self, use_hip: bool = True, decode_workspace: torch.Tensor | None = None):
-        """decode_workspace (not in the reference): a decode workspace (page
-        prefix sum + split partials, see paged_decode_attention) for this
-        backend's decode calls instead of the per-stream cached one; a graph
-        capture passes its own, sized for its largest batch."""
+        """decode_workspace (not in the reference): a workspace (page prefix
+        sum + split partials, see paged_decode_attention) for this backend's
+        decode and verify-form prefill calls instead of the per-stream cached
+        one; a graph capture passes its own, sized for its largest batch."""
         if not use_hip:
             raise ValueError("nimbus_amd's AttentionBackend is the HIP path only; use Nimbus's reference "
                              "backend for CPU execution")
@@ -92,13 +96,17 @@ class AttentionBackend:
         out = torch.empty_like(q)
         p = meta.num_prefill_tokens
         if p:
-            if meta.prefill_programs is None:
+            if meta.prefill_kernel is None:
+                nq = prefill_attention.verify_queries(meta.prefill_query_start_host, q.shape[1], k_cache.shape[2])
+                meta.prefill_kernel = "verify" if nq else "tile"
+            if meta.prefill_programs is None and meta.prefill_kernel == "tile":
                 meta.prefill_programs = self._build_programs(meta.prefill_query_start_host, q.device,
                                                              meta.prefill_context_lens_host)
             self._prefill(
                 q[:p], k_cache, v_cache, meta.prefill_query_start, meta.prefill_context_lens,
                 meta.prefill_block_tables, scale, meta.prefill_query_start_host,
                 meta.prefill_context_lens_host, meta.prefill_programs, out=out[:p],
+                workspace=self.decode_workspace, kernel=meta.prefill_kernel,
             )
         if meta.num_decodes:
             self._decode(

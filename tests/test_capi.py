@@ -23,7 +23,8 @@ def declared_functions() -> list[str]:
 def test_header_declares_the_four_launch_paths():
     names = declared_functions()
     for want in ("nimbus_write_kv", "nimbus_paged_decode", "nimbus_paged_decode_workspace_bytes",
-                 "nimbus_paged_prefill", "nimbus_add_rms_norm", "nimbus_attn_abi_version",
+                 "nimbus_paged_prefill", "nimbus_paged_verify", "nimbus_paged_verify_workspace_bytes",
+                 "nimbus_add_rms_norm", "nimbus_attn_abi_version",
                  "nimbus_attn_error_string"):
         assert want in names
 
@@ -71,6 +72,18 @@ def test_workspace_bytes_is_a_pure_size_formula():
     assert f(-1, 32, 128, 8192) == -1
 
 
+def test_verify_workspace_scales_the_decode_formula_by_queries():
+    """A verify call holds pieces for queries_per_seq columns per head: the
+    decode workspace of queries_per_seq x num_heads heads."""
+    lib = _lib.load()
+    f, dec = lib.nimbus_paged_verify_workspace_bytes, lib.nimbus_paged_decode_workspace_bytes
+    assert f(16, 1, 32, 128, 8192) == dec(16, 32, 128, 8192)
+    assert f(16, 5, 32, 128, 8192) == dec(16, 160, 128, 8192)
+    assert f(3, 16, 8, 64, 100) == dec(3, 128, 64, 100)
+    for bad in (0, 17, -1):
+        assert f(16, bad, 32, 128, 8192) == -1
+
+
 DUMMY = 1 << 20  # a 16-byte aligned fake address: these calls must return before touching it
 
 
@@ -98,6 +111,27 @@ def _decode(**kw):
 ])
 def test_decode_argument_checks(kw, code):
     assert _decode(**kw) == code
+
+
+def test_verify_argument_checks():
+    """queries_per_seq outside 1..16 is refused; the rest are the decode
+    checks, with the workspace sized for every query column."""
+    lib = _lib.load()
+
+    def verify(nq, **kw):
+        a = dict(q=DUMMY, qsb=32 * 128, qsh=128, k=DUMMY, v=DUMMY, nb=100, csb=16 * 8 * 128, cst=8 * 128, csh=128,
+                 bt=DUMMY, bts=4, btw=4, ctx=DUMMY, out=DUMMY, osb=32 * 128, osh=128, ws=None, wsb=0, b=2, h=32,
+                 kv=8, d=128, bs=16, maxc=64, scale=0.1, dt=1, stream=None)
+        a.update(kw)
+        return lib.nimbus_paged_verify(nq, *a.values())
+
+    assert verify(0) == _lib.NIMBUS_ERR_INVALID
+    assert verify(17) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert verify(5, bs=8) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert verify(5, b=0) == 0
+    # a workspace big enough for decode is too small for five query columns
+    dec = lib.nimbus_paged_decode_workspace_bytes(2, 32, 128, 64)
+    assert verify(5, ws=DUMMY, wsb=dec) == _lib.NIMBUS_ERR_WORKSPACE
 
 
 def test_prefill_and_write_kv_argument_checks():

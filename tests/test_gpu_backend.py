@@ -113,9 +113,12 @@ def test_verify_graph_replay_matches_eager_and_oracle(n, q_len, dtype):
     q_len = k + 1 new tokens on cached contexts, captured once per padded size
     with the precomputed tile table (arange(b), zeros(b)) and placeholder host
     lists. Each replay, with eager work and synchronisations between
-    replays, is bit-identical to the eager backend call on the same
-    sequences (every prefill unit is independent of the tile order and of
-    the padding units), writes the same cache, and matches the oracle."""
+    replays, is bit-identical to the eager backend call on the padded batch
+    with the graph's metadata (same kernels, same grid), within the bar of
+    the eager call on the unpadded batch (the verify form splits pages
+    between waves by batch and table width), writes the same cache, and
+    matches the oracle. q_len 5 takes the verify form, q_len 16 at G = 8
+    the tile kernel."""
     announce(f"verify graph n={n} q_len={q_len} dtype={dtype}")
     g = torch.Generator().manual_seed(n * 100 + q_len)
     ctx = [int(c) for c in torch.randint(q_len + 1, 3000, (n,), generator=g)]
@@ -142,8 +145,16 @@ def test_verify_graph_replay_matches_eager_and_oracle(n, q_len, dtype):
         replays.append(graphs.run(b.q, b.k, b.v, b.slot_mapping, pa[4], b.block_tables).clone())
         torch.cuda.synchronize()
         _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # eager work between replays
+    bp = graphs.padded_size(n)
+    padded_meta = graphs.graphs[bp][2]
+    assert padded_meta.prefill_kernel == ("verify" if q_len * heads // kv <= 32 else "tile")
+    kc_p, vc_p = kc.clone(), vc.clone()
+    rows = bp * q_len
+    padded = AttentionBackend(decode_workspace=graphs.backend.decode_workspace).forward(
+        graphs.q[:rows], graphs.k[:rows], graphs.v[:rows], kc_p, vc_p, padded_meta, b.scale)[:n * q_len]
     for rep, got in enumerate(replays):
-        assert torch.equal(got, eager), f"replay {rep} differs from the eager call"
+        assert torch.equal(got, padded), f"replay {rep} differs from eager on the padded batch"
+        assert_within(got.cpu(), eager.cpu().double(), what=f"replay {rep} vs eager")
     assert torch.equal(kc[:nb], kc_e[:nb]) and torch.equal(vc[:nb], vc_e[:nb])
     want = oracle_prefill(b.q, kc_e, vc_e, pa[7], pa[8], b.block_tables, b.scale)
     assert_within(replays[0].cpu(), want, what="verify replay vs oracle")

@@ -37,12 +37,13 @@ def _case(heads, kv, d, seqs, dtype, seed=1, pool=None):
 REF_SEQS = [[(5, 5), (64, 64), (130, 130)], [(3, 40), (17, 17), (1, 9), (70, 200)], [(1, 1)]]
 
 
+@pytest.mark.parametrize("kernel", ["auto", "tile"])  # auto: [(1, 1)] takes the verify form
 @pytest.mark.parametrize("heads,kv", [(32, 4), (8, 8)])
 @pytest.mark.parametrize("seqs", REF_SEQS)
-def test_reference_matrix_fp16_d64(heads, kv, seqs):
-    announce(f"prefill ref-matrix H={heads} KV={kv} seqs={seqs}")
+def test_reference_matrix_fp16_d64(heads, kv, seqs, kernel):
+    announce(f"prefill ref-matrix H={heads} KV={kv} seqs={seqs} kernel={kernel}")
     args = _case(heads, kv, 64, seqs, torch.float16, pool=400)
-    got = paged_prefill_attention(*args)
+    got = paged_prefill_attention(*args, kernel=kernel)
     q, k, v, _, _, bt, scale, qs, ctx = args
     want = oracle_prefill(q, k, v, qs, ctx, bt, scale)
     assert_within(got.cpu(), want, what="vs oracle (fp32 accumulation)")

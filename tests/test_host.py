@@ -66,7 +66,29 @@ def test_attn_metadata_fields_match_reference():
     want = ["slot_mapping", "num_prefill_tokens", "prefill_query_start", "prefill_context_lens",
             "prefill_block_tables", "decode_context_lens", "decode_block_tables", "max_decode_context",
             "prefill_query_start_host", "prefill_context_lens_host", "prefill_programs", "decode_partitions"]
-    assert [f.name for f in dataclasses.fields(AttnMetadata)] == want
+    names = [f.name for f in dataclasses.fields(AttnMetadata)]
+    assert names[:len(want)] == want
+    assert names[len(want):] == ["prefill_kernel"]  # ours, defaulted, after the reference's fields
+
+
+@pytest.mark.parametrize("qs,heads,kv,want", [
+    ([0, 5, 10, 15], 32, 8, 5),     # k = 4 draft tokens, Llama-3-8B groups: 20 columns
+    ([0, 8, 16], 32, 8, 8),         # 32 columns: the limit
+    ([0, 9, 18], 32, 8, 0),         # 36 columns: the tile kernel
+    ([0, 5, 10, 16], 32, 8, 0),     # ragged
+    ([0, 1], 32, 32, 1),            # one token, MHA
+    ([0, 17, 34], 8, 8, 0),         # more queries than a page
+    ([0], 32, 8, 0),                # no sequences
+    ([0, 3, 6, 9], 12, 4, 3),
+])
+def test_verify_form_takes_uniform_short_runs(qs, heads, kv, want):
+    assert prefill_attention.verify_queries(qs, heads, kv) == want
+
+
+def test_verify_form_batch_limit():
+    n = prefill_attention.MAX_VERIFY_SEQUENCES
+    assert prefill_attention.verify_queries(list(range(0, 2 * (n + 1), 2)), 32, 8) == 2
+    assert prefill_attention.verify_queries(list(range(0, 2 * (n + 2), 2)), 32, 8) == 0
 
 
 def test_backend_has_no_cpu_path():
