@@ -427,13 +427,19 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
 
 // Second pass: for every sequence whose pages were split between waves,
 // o = sum_i O_i w_i / sum_i L_i w_i with w_i = 2^(m_i - max m) over its
-// pieces (nimbus/kernels/paged_attention.py:83-98), in one pass with a
-// running max. One wave per (sequence, kv-head group): lane = (column of
-// the group, 8 consecutive elements of d); sequences held whole by one wave
-// exit at once.
+// pieces (nimbus/kernels/paged_attention.py:83-98). One workgroup per
+// (sequence, kv-head group), one lane per (column of the group, 8
+// consecutive elements of d); sequences held whole by one wave exit at once.
+// A long sequence has tens of pieces, so they are read kMergeBatch at a time,
+// every load of a batch issued before any is used: the pass costs a few
+// memory round trips instead of one per piece.
+constexpr int kMergeBatch = 8;
+constexpr int kMergeThreads = 256;  // 16 columns x D / 8 lanes (D <= 128)
+
 template <int DT, int D>
-__global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
-  constexpr int SEG = D / 8;  // lanes per head
+__global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(DecodeArgs a) {
+  constexpr int SEG = D / 8;  // lanes per column
+  static_assert(16 * SEG <= kMergeThreads, "one lane per (column, 8 elements of d)");
   const int b = blockIdx.x;
   const int kg = blockIdx.y;
   const int total = a.pre_out[a.B];
@@ -447,41 +453,60 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   const int kvh = kg % a.nkv;
   const int g0 = (kg / a.nkv) * 16;
   const int gcount = min(16, a.nq * a.G - g0);
-  for (int e = threadIdx.x; e < gcount * SEG; e += 64) {
-    const int vcol = g0 + e / SEG;
-    const int qj = vcol / a.G;
-    const int head = kvh * a.G + vcol - qj * a.G;
-    const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;
-    const int d0 = 8 * (e % SEG);
-    float M = -INFINITY, L = 0.f;
-    float O[8];
+  const int e = threadIdx.x;
+  if (e >= gcount * SEG) return;
+  const int vcol = g0 + e / SEG;
+  const int qj = vcol / a.G;
+  const int head = kvh * a.G + vcol - qj * a.G;
+  const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;
+  const int64_t cols = static_cast<int64_t>(a.nq) * a.H;  // rows per slot
+  const int d0 = 8 * (e % SEG);
+
+  float M = kNoScore, L = 0.f;
+  float O[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) O[k] = 0.f;
-    for (int i = i0; i <= i1; ++i) {
-      const int64_t row = (static_cast<int64_t>(i) + b) * a.nq * a.H + vhead;
-      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
-      const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
-      const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
-      const float Mn = fmaxf(M, ml.x);
-      const float wo = fast_exp2(M - Mn);
-      const float wi = fast_exp2(ml.x - Mn);
-      M = Mn;
-      L = L * wo + ml.y * wi;
+  for (int k = 0; k < 8; ++k) O[k] = 0.f;
+  for (int i = i0; i <= i1; i += kMergeBatch) {
+    float2 ml[kMergeBatch];
+    f32x4 o0[kMergeBatch], o1[kMergeBatch];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        O[k] = O[k] * wo + o0[k] * wi;
-        O[k + 4] = O[k + 4] * wo + o1[k] * wi;
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const int64_t row = (static_cast<int64_t>(min(i + u, i1)) + b) * cols + vhead;
+      ml[u] = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+      o0[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
+      o1[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
+    }
+    float mx = M;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      if (i + u <= i1) mx = fmaxf(mx, ml[u].x);
+    }
+    const float wo = fast_exp2(M - mx);
+    L *= wo;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) O[k] *= wo;
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      if (i + u <= i1) {
+        const float wi = fast_exp2(ml[u].x - mx);
+        L += ml[u].y * wi;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          O[k] += o0[u][k] * wi;
+          O[k + 4] += o1[u][k] * wi;
+        }
       }
     }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    const int64_t tok = static_cast<int64_t>(b) * a.nq + qj;
-    uint16_t* orow = a.out + tok * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
-    const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O[0] * inv), Elem<DT>::from_f32(O[1] * inv)),
-                          pack2(Elem<DT>::from_f32(O[2] * inv), Elem<DT>::from_f32(O[3] * inv)),
-                          pack2(Elem<DT>::from_f32(O[4] * inv), Elem<DT>::from_f32(O[5] * inv)),
-                          pack2(Elem<DT>::from_f32(O[6] * inv), Elem<DT>::from_f32(O[7] * inv))};
-    *reinterpret_cast<u32x4*>(orow) = w;
+    M = mx;
   }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const int64_t tok = static_cast<int64_t>(b) * a.nq + qj;
+  uint16_t* orow = a.out + tok * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
+  const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O[0] * inv), Elem<DT>::from_f32(O[1] * inv)),
+                        pack2(Elem<DT>::from_f32(O[2] * inv), Elem<DT>::from_f32(O[3] * inv)),
+                        pack2(Elem<DT>::from_f32(O[4] * inv), Elem<DT>::from_f32(O[5] * inv)),
+                        pack2(Elem<DT>::from_f32(O[6] * inv), Elem<DT>::from_f32(O[7] * inv))};
+  *reinterpret_cast<u32x4*>(orow) = w;
 }
 
 // Waves the launch gives each kv-head group: what the chip keeps resident,
@@ -509,7 +534,7 @@ static int launch_decode(const DecodeArgs& a, int phases, hipStream_t stream) {
     hipLaunchKernelGGL((paged_decode_kernel<DT, D>), dim3(a.nwk * a.kvg), dim3(64), dyn, stream, a);
   }
   if (phases & 2) {
-    hipLaunchKernelGGL((paged_decode_merge_kernel<DT, D>), dim3(a.B, a.kvg), dim3(64), 0, stream, a);
+    hipLaunchKernelGGL((paged_decode_merge_kernel<DT, D>), dim3(a.B, a.kvg), dim3(kMergeThreads), 0, stream, a);
   }
   return static_cast<int>(hipGetLastError());
 }
