@@ -30,6 +30,10 @@ verify       speculative verification's attention (16 sequences x 5 tokens)
 add_rms_norm the fused residual add + RMSNorm at three model shapes:
              algorithmic bytes (x and residual read, residual and output
              written, weight once) / mean kernel time, against 8 TB/s
+int8_matmul  the INT8 weight-only matmul at Llama-3-8B decode projections
+             (and Nimbus's own TinyLlama bench shape): algorithmic bytes
+             (int8 weights, x, y, scales) / mean kernel time, against 8 TB/s,
+             beside torch's dense matmul on the dequantized weights
 
 Between timed calls the K/V pool rotates over enough copies (>= 1.5 GB) that
 the 256 MB Infinity Cache cannot serve one call's pages to the next.
@@ -393,6 +397,73 @@ def time_add_rms_norm(steps, warmup):
     return res
 
 
+# ---------------------------------------------------------------- INT8 weight-only matmul
+
+INT8_SHAPES = (
+    # name, tokens, out channels N, in channels K, dtype
+    ("llama3 qkv_proj, 64 tokens (config-3 decode batch)", 64, 6144, 4096, "bfloat16"),
+    ("llama3 o_proj, 64 tokens", 64, 4096, 4096, "bfloat16"),
+    ("llama3 gate_up_proj, 64 tokens", 64, 28672, 4096, "bfloat16"),
+    ("llama3 down_proj, 64 tokens", 64, 4096, 14336, "bfloat16"),
+    ("llama3 gate_up_proj, 1 token", 1, 28672, 4096, "bfloat16"),
+    ("tinyllama gate_up_proj, 16 tokens, fp16 (Nimbus's kernel bench shape)", 16, 11264, 2048, "float16"),
+)
+
+
+def _graph_us(calls, steps, warmup):
+    """Mean time of one call of `calls` (a list of thunks) captured back to
+    back in one hipGraph and replayed."""
+    import torch
+
+    for c in calls[:2]:
+        c()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    for _ in range(warmup):
+        graph.replay()
+    per = statistics.mean(event_times_us(lambda i: graph.replay(), max(3, steps // 10), torch.cuda.current_stream()))
+    del graph
+    return per / len(calls)
+
+
+def time_int8_matmul(steps, warmup):
+    """int8_matmul at decode shapes: algorithmic bytes (the int8 weights, x,
+    y and the scales once) per kernel time, against 8 TB/s, and beside it
+    torch's dense matmul (hipBLASLt) on the same weights dequantized to the
+    activation dtype, the comparison of Nimbus's own kernel bench
+    (int8 vs fp16 cuBLAS). Calls run back to back in a hipGraph over
+    weight copies totalling >= 1 GB, so no call finds its weights in the
+    256 MB Infinity Cache."""
+    import torch
+
+    from nimbus_amd.kernels.int8_matmul import int8_matmul, int8_matmul_workspace_bytes
+    from nimbus_amd.quant import dequantize_weight, quantize_weight
+
+    res = []
+    for name, m, n, k, dt in INT8_SHAPES:
+        dtype = getattr(torch, dt)
+        n_pools = max(4, int(math.ceil(1e9 / (n * k))))
+        g = torch.Generator(device="cuda").manual_seed(n + k)
+        pools = [quantize_weight((torch.randn(n, k, generator=g, device="cuda") * 0.02).to(dtype))
+                 for _ in range(n_pools)]
+        x = torch.randn(m, k, generator=g, device="cuda").to(dtype)
+        out = torch.empty(m, n, dtype=dtype, device="cuda")
+        ws = torch.empty(max(256, int8_matmul_workspace_bytes(m, n, k)), dtype=torch.uint8, device="cuda")
+        us = _graph_us([lambda q=q, s=s: int8_matmul(x, q, s, out=out, workspace=ws) for q, s in pools],
+                       steps, warmup)
+        nbytes = n * k + 2 * m * k + 2 * m * n + 2 * n
+        dense = [dequantize_weight(q, s) for q, s in pools[:max(2, n_pools // 2)]]  # 2 bytes a weight
+        dus = _graph_us([lambda d=d: torch.matmul(x, d.T, out=out) for d in dense], steps, warmup)
+        res.append({"shape": name, "m": m, "n": n, "k": k, "dtype": dt, "us_per_call": us, "bytes": nbytes,
+                    "GBps": nbytes / us / 1e3, "frac_hbm_peak": nbytes / us / 1e3 / HBM_PEAK_GBS,
+                    "dense_matmul_us": dus, "speedup_vs_dense": dus / us, "calls_per_replay": n_pools})
+        del pools, dense
+    return res
+
+
 # ---------------------------------------------------------------- --all
 
 def all_configs(steps, warmup):
@@ -504,6 +575,9 @@ def main(argv=None):
         log("add_rms_norm")
         result["add_rms_norm"] = time_add_rms_norm(args.steps, args.warmup)
         log(f"add_rms_norm: {result['add_rms_norm']}")
+        log("int8_matmul")
+        result["int8_matmul"] = time_int8_matmul(args.steps, args.warmup)
+        log(f"int8_matmul: {result['int8_matmul']}")
     if args.all:
         result["configs"] = {k: {a: b for a, b in v.items() if not isinstance(b, dict)}
                              for k, v in all_configs(args.steps, args.warmup).items()}

@@ -3,8 +3,9 @@
  *
  * libnimbus_attn.so replaces the GPU side of Nimbus's attention hot path:
  * the KV slot write, paged decode attention, causal varlen paged prefill
- * attention (with a verify form for uniform short query runs), and the
- * fused residual add + RMSNorm on either side of it. Every entry point
+ * attention (with a verify form for uniform short query runs), the fused
+ * residual add + RMSNorm on either side of it, and the INT8 weight-only
+ * matmul of the quantized projections. Every entry point
  * takes plain device pointers, element strides
  * (not bytes), sizes, a dtype code and an opaque hipStream_t; none allocates,
  * frees, synchronises or reads device memory on the host, so each call can be
@@ -27,7 +28,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 4
+#define NIMBUS_ATTN_ABI_VERSION 5
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -38,7 +39,7 @@ extern "C" {
 #define NIMBUS_ERR_INVALID (-1)     /* inconsistent sizes or null pointers */
 #define NIMBUS_ERR_UNSUPPORTED (-2) /* shape/dtype outside what the kernels cover */
 #define NIMBUS_ERR_ALIGNMENT (-3)   /* a base or stride breaks 16-byte vector access */
-#define NIMBUS_ERR_WORKSPACE (-4)   /* decode workspace missing or too small */
+#define NIMBUS_ERR_WORKSPACE (-4)   /* workspace missing or too small */
 
 /* Version of this ABI (NIMBUS_ATTN_ABI_VERSION). */
 int nimbus_attn_abi_version(void);
@@ -194,6 +195,29 @@ int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* residual, i
                         const void* weight, void* out, int64_t out_stride, void* residual_out,
                         int64_t residual_out_stride, int64_t rows, int32_t cols, float eps, int32_t dtype,
                         void* stream);
+
+/*
+ * Bytes of workspace nimbus_int8_matmul needs for an [m, k] x [n, k]^T
+ * product (0 when it runs without one): a pure function of the shape. The
+ * workspace carries nothing between calls; concurrent calls need their own.
+ */
+int64_t nimbus_int8_matmul_workspace_bytes(int64_t m, int32_t n, int32_t k);
+
+/*
+ * INT8 weight-only matmul. Replaces nimbus/kernels/int8_matmul.py:26-64
+ * (the Triton _int8_matmul_kernel behind int8_matmul, run by Int8Linear,
+ * nimbus/quant/int8.py:32-47):
+ *   y[i, j] = dtype(fp32(sum_k x[i, k] * w_q[j, k]) * scale[j])
+ * x [m, k] and y [m, n] in dtype with row strides x_stride / y_stride
+ * (elements); w_q int8 [n, k] with row stride w_stride (bytes); scale [n]
+ * in dtype. n must be a multiple of 4 and k of 16; x, w_q and y 16-byte
+ * aligned, scale 8-byte aligned, x_stride a multiple of 8, w_stride of 16,
+ * y_stride of 4; x and w_q each under 2 GiB. The summation order over k
+ * depends only on the shape, so equal inputs give equal outputs.
+ */
+int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w_q, int64_t w_stride, const void* scale,
+                       void* y, int64_t y_stride, int64_t m, int32_t n, int32_t k, void* workspace,
+                       int64_t workspace_bytes, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,342 @@
+// INT8 weight-only matmul for gfx950: y = dtype(fp32(x @ w_q^T) * scale).
+//
+// Replaces nimbus/kernels/int8_matmul.py:26-64 (the Triton
+// _int8_matmul_kernel and its wrapper), which Int8Linear
+// (nimbus/quant/int8.py:32-47) runs for the decoder projections. x is fp16
+// or bf16 [M, K]; w_q int8 [N, K] (round(w / scale), |w_q| <= 127, per
+// output channel); scale [N] in x's dtype; y [M, N] in x's dtype.
+//
+// Decode is bound by reading the weights, so every weight byte is streamed
+// from HBM once per launch:
+// - a workgroup of 8 waves owns 128 output channels, 16 per wave (the rows
+//   of a 16x16x32 MFMA's A operand), over one range of K;
+// - each lane loads 16 consecutive int8 of its row per 64-k step, kRing
+//   steps ahead, and converts them exactly to fp16 / bf16 in registers
+//   (|w_q| <= 127 fits either type's significand);
+// - x's 64-k step for the workgroup's tokens is staged in LDS once and read
+//   by all 8 waves; its global loads ride the same kRing-deep register ring
+//   as the weights, so waiting for one never drains the other;
+// - the k order inside a step is the same permutation for both operands, so
+//   one 16-byte weight load feeds two MFMAs: chunk 0 takes k = 16g + 0..7 of
+//   lane group g, chunk 1 takes k = 16g + 8..15 (the sum over k does not
+//   depend on the order).
+// When the output channels alone would leave CUs idle, K is split between
+// workgroups: each writes its fp32 partial sums, and
+// int8_matmul_reduce_kernel adds them in split order (the result does not
+// depend on timing), scales and rounds.
+#include "common.h"
+#include "nimbus_attn_internal.h"
+
+namespace nimbus {
+
+constexpr int kGemmWaves = 8;
+constexpr int kGemmThreads = 64 * kGemmWaves;
+constexpr int kGemmRows = 16 * kGemmWaves;  // output channels per workgroup
+constexpr int kGemmStep = 64;               // k per pipeline step
+constexpr int kGemmRing = 8;                // steps of loads in flight
+// One token's step of x in LDS: 128 bytes + 16 of padding, so the 16 tokens
+// an MFMA reads (one per lane of a 16-lane group) start 36 banks apart and
+// their 16-byte reads cover all 64 banks once.
+constexpr int kXRow = 2 * kGemmStep + 16;
+constexpr int kMaxSplits = 16;
+constexpr int kMinSplitK = kGemmRing * kGemmStep;  // splits are whole rings of steps
+constexpr int kFillWorkgroups = 256;        // one per CU of a gfx950 part
+
+constexpr int32_t kBufferFlags = 0x00020000;     // raw buffer descriptor word 3 for gfx950
+constexpr uint32_t kOutOfRange = 0xFFFFFFF0u;     // a buffer offset past any operand: reads zero
+
+struct GemmArgs {
+  const uint16_t* x;
+  int32_t sx;        // elements; x spans x_bytes < 2^31
+  const int8_t* w;
+  int32_t sw;        // bytes; w spans w_bytes < 2^31
+  int32_t x_bytes, w_bytes;
+  const uint16_t* scale;
+  uint16_t* y;
+  int64_t sy;
+  float* part;  // [splits][M][N] fp32 partial sums (splits > 1)
+  int32_t M, N, K;
+  int32_t splits, ksplit;  // ksplit: k per split, a multiple of kMinSplitK
+};
+
+typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
+
+// Eight int8 (two dwords) -> the eight fp16 / bf16 of an MFMA operand.
+template <int DT>
+__device__ __forceinline__ u32x4 i8x8_to_operand(uint32_t w0, uint32_t w1);
+
+// fp16: byte b + 128 goes under the exponent of 1024 (0x64XX is 1024 + XX)
+// and 1152 is subtracted; both steps are exact.
+__device__ __forceinline__ u32x2 i8x4_to_f16x4(uint32_t w) {
+  const uint32_t u = w ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [1024 + u0, 1024 + u1]
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [1024 + u2, 1024 + u3]
+  const h16x2 bias = h16x2{static_cast<_Float16>(-1152.f), static_cast<_Float16>(-1152.f)};
+  return u32x2{__builtin_bit_cast(uint32_t, __builtin_bit_cast(h16x2, lo) + bias),
+               __builtin_bit_cast(uint32_t, __builtin_bit_cast(h16x2, hi) + bias)};
+}
+
+template <>
+__device__ __forceinline__ u32x4 i8x8_to_operand<kFloat16>(uint32_t w0, uint32_t w1) {
+  const u32x2 a = i8x4_to_f16x4(w0), b = i8x4_to_f16x4(w1);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// bf16: byte b + 128 goes under the fp32 exponent of 2^23 and 2^23 + 128 is
+// subtracted (exact); the upper half of that fp32 is b's bf16, exactly.
+__device__ __forceinline__ u32x2 i8x4_to_bf16x4(uint32_t w) {
+  const uint32_t u = w ^ 0x80808080u;
+  float f[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // bytes [u_i, 0, 0, 0x4B] of (src0 = 0x4B000000, src1 = u)
+    const uint32_t bits = __builtin_amdgcn_perm(0x4B000000u, u, 0x07060500u | static_cast<uint32_t>(i));
+    f[i] = __uint_as_float(bits) - 8388736.f;
+  }
+  // upper halves of (f0, f1) and (f2, f3)
+  return u32x2{__builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u),
+               __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u)};
+}
+
+template <>
+__device__ __forceinline__ u32x4 i8x8_to_operand<kBFloat16>(uint32_t w0, uint32_t w1) {
+  const u32x2 a = i8x4_to_bf16x4(w0), b = i8x4_to_bf16x4(w1);
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// Workgroup barrier that waits only for LDS traffic, so the weight loads in
+// flight stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Grid: (N / 128 channel tiles, splits, M / BM token tiles).
+template <int DT, int BM>
+__global__ __launch_bounds__(kGemmThreads) void int8_matmul_kernel(GemmArgs a) {
+  constexpr int CB = BM / 16;   // 16-token column blocks
+  constexpr int XT = BM * 8;    // threads staging x: one 16-byte chunk of a token's step each
+  static_assert(XT <= kGemmThreads, "x staging needs one thread per chunk");
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][BM * kXRow];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int lane = tid % 64;
+  const int col = lane % 16;
+  const int grp = lane / 16;
+  const int n0 = blockIdx.x * kGemmRows + 16 * wave;
+  const int kb = blockIdx.y * a.ksplit;
+  const int ke = min(a.K, kb + a.ksplit);
+  const int m0 = blockIdx.z * BM;
+  const int steps = (ke - kb + kGemmStep - 1) / kGemmStep;
+
+  // Loads are unconditional buffer loads: a masked lane's offset is past the
+  // buffer's end and reads zeros, so no branch (and no full wait for the
+  // loads in flight) is needed to skip it.
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(a.w), 0, __builtin_amdgcn_readfirstlane(a.w_bytes), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), 0, __builtin_amdgcn_readfirstlane(a.x_bytes), kBufferFlags);
+  // This lane's weight row (rows past N read row N - 1 and are never stored).
+  const uint32_t woff = static_cast<uint32_t>(min(n0 + col, a.N - 1) * a.sw + kb + 16 * grp);
+  auto load_w = [&](int s) {
+    const bool on = kb + kGemmStep * s + 16 * grp < ke;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         wrsrc, on ? woff + kGemmStep * s : kOutOfRange, 0, 0));
+  };
+  // x staging: thread t < XT moves token t / 8, 16-byte chunk t % 8 of each
+  // step; tokens past M and k past the range stage zeros.
+  const int xt_tok = tid / 8;
+  const int xt_chunk = tid % 8;
+  const bool xt_on = tid < XT && m0 + xt_tok < a.M;
+  const uint32_t xoff = xt_on ? static_cast<uint32_t>(2 * ((m0 + xt_tok) * a.sx + kb + 8 * xt_chunk)) : 0u;
+  auto load_x = [&](int s) {
+    const bool on = xt_on && kb + kGemmStep * s + 8 * xt_chunk < ke;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         xrsrc, on ? xoff + 2 * kGemmStep * s : kOutOfRange, 0, 0));
+  };
+  const int xs_off = xt_tok * kXRow + 16 * xt_chunk;
+
+  u32x4 wr[kGemmRing], xr[kGemmRing];
+#pragma unroll
+  for (int j = 0; j < kGemmRing; ++j) {
+    wr[j] = load_w(j);
+    xr[j] = load_x(j);
+  }
+  if (tid < XT) *reinterpret_cast<u32x4*>(&xs[0][xs_off]) = xr[0];
+  lds_barrier();
+
+  f32x4 acc[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int xb_off = col * kXRow + 32 * grp;  // B operand: token col of a block, bytes 32 grp .. +32
+
+  // Whole rings of steps: a step past the range loads zeros (out-of-range
+  // offsets) for both operands and adds exactly 0, and the ring's registers
+  // keep their places across iterations (no copies that would wait for
+  // loads in flight).
+  for (int s0 = 0; s0 < steps; s0 += kGemmRing) {
+#pragma unroll
+    for (int j = 0; j < kGemmRing; ++j) {
+      const int s = s0 + j;
+      const uint8_t* xb = &xs[s & 1][xb_off];
+      const u32x4 wv = wr[j];
+      const u32x4 a0 = i8x8_to_operand<DT>(wv[0], wv[1]);
+      const u32x4 a1 = i8x8_to_operand<DT>(wv[2], wv[3]);
+      // Refill this ring slot: x(s) left it for LDS at the end of step s - 1.
+      wr[j] = load_w(s + kGemmRing);
+      xr[j] = load_x(s + kGemmRing);
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const u32x4 b0 = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow);
+        const u32x4 b1 = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow + 16);
+        acc[cb] = mfma_16x16x32<DT>(a0, b0, acc[cb]);
+        acc[cb] = mfma_16x16x32<DT>(a1, b1, acc[cb]);
+      }
+      // Stage x(s + 1) in the other buffer: every wave finished reading it
+      // (step s - 1) before the last barrier.
+      if (tid < XT) *reinterpret_cast<u32x4*>(&xs[(s + 1) & 1][xs_off]) = xr[(j + 1) % kGemmRing];
+      lds_barrier();
+    }
+  }
+
+  // Lane (col, grp) holds token m0 + 16 cb + col, channels n0 + 4 grp + r.
+  const int n = n0 + 4 * grp;
+  if (n >= a.N) return;
+  if (a.splits == 1) {
+    const u32x2 sw = *reinterpret_cast<const u32x2*>(a.scale + n);
+    const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
+                         Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int m = m0 + 16 * cb + col;
+      if (m < a.M) {
+        const f32x4 o = acc[cb];
+        const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(o[0] * sc[0]), Elem<DT>::from_f32(o[1] * sc[1])),
+                              pack2(Elem<DT>::from_f32(o[2] * sc[2]), Elem<DT>::from_f32(o[3] * sc[3]))};
+        *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int m = m0 + 16 * cb + col;
+      if (m < a.M) {
+        float* p = a.part + (static_cast<int64_t>(blockIdx.y) * a.M + m) * a.N + n;
+        *reinterpret_cast<f32x4*>(p) = acc[cb];
+      }
+    }
+  }
+}
+
+// Sum of the split partials in split order, scaled and rounded: one thread
+// per 4 consecutive outputs of a row.
+template <int DT>
+__global__ __launch_bounds__(256) void int8_matmul_reduce_kernel(GemmArgs a) {
+  const int64_t quads = static_cast<int64_t>(a.M) * (a.N / 4);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= quads) return;
+  const int m = static_cast<int>(i / (a.N / 4));
+  const int n = static_cast<int>(i % (a.N / 4)) * 4;
+  const int64_t plane = static_cast<int64_t>(a.M) * a.N;
+  const float* p = a.part + static_cast<int64_t>(m) * a.N + n;
+  f32x4 s = *reinterpret_cast<const f32x4*>(p);
+  for (int k = 1; k < a.splits; ++k) s += *reinterpret_cast<const f32x4*>(p + k * plane);
+  const u32x2 sw = *reinterpret_cast<const u32x2*>(a.scale + n);
+  const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
+                       Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
+  const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(s[0] * sc[0]), Elem<DT>::from_f32(s[1] * sc[1])),
+                        pack2(Elem<DT>::from_f32(s[2] * sc[2]), Elem<DT>::from_f32(s[3] * sc[3]))};
+  *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
+}
+
+// Tokens per workgroup tile for M tokens.
+static int gemm_bm(int64_t m) { return m <= 16 ? 16 : (m <= 32 ? 32 : 64); }
+
+// K split: enough workgroups to give every CU one, each split a whole number
+// of rings of steps. A pure function of the shape.
+static void gemm_split(int64_t m, int32_t n, int32_t k, int32_t* splits, int32_t* ksplit) {
+  const int64_t tiles = ((n + kGemmRows - 1) / kGemmRows) * ((m + gemm_bm(m) - 1) / gemm_bm(m));
+  int64_t s = 1;
+  if (tiles < kFillWorkgroups) s = (kFillWorkgroups + tiles - 1) / tiles;
+  if (s > kMaxSplits) s = kMaxSplits;
+  if (s > k / kMinSplitK) s = k / kMinSplitK;
+  if (s < 1) s = 1;
+  int64_t ks = (k + s - 1) / s;
+  ks = (ks + kMinSplitK - 1) / kMinSplitK * kMinSplitK;
+  *ksplit = static_cast<int32_t>(ks);
+  *splits = static_cast<int32_t>((k + ks - 1) / ks);
+}
+
+template <int DT, int BM>
+static int launch_gemm(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid((a.N + kGemmRows - 1) / kGemmRows, a.splits, (a.M + BM - 1) / BM);
+  hipLaunchKernelGGL((int8_matmul_kernel<DT, BM>), grid, dim3(kGemmThreads), 0, s, a);
+  if (a.splits > 1) {
+    const int64_t quads = static_cast<int64_t>(a.M) * (a.N / 4);
+    hipLaunchKernelGGL((int8_matmul_reduce_kernel<DT>), dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256),
+                       0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int DT>
+static int launch_gemm_dt(const GemmArgs& a, hipStream_t s) {
+  switch (gemm_bm(a.M)) {
+    case 16: return launch_gemm<DT, 16>(a, s);
+    case 32: return launch_gemm<DT, 32>(a, s);
+    default: return launch_gemm<DT, 64>(a, s);
+  }
+}
+
+}  // namespace nimbus
+
+using namespace nimbus;
+
+extern "C" int64_t nimbus_int8_matmul_workspace_bytes(int64_t m, int32_t n, int32_t k) {
+  if (m < 0 || n <= 0 || k <= 0) return -1;
+  int32_t splits = 1, ksplit = 0;
+  gemm_split(m, n, k, &splits, &ksplit);
+  return splits > 1 ? static_cast<int64_t>(splits) * m * n * 4 : 0;
+}
+
+extern "C" int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w_q, int64_t w_stride,
+                                  const void* scale, void* y, int64_t y_stride, int64_t m, int32_t n, int32_t k,
+                                  void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream) {
+  if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (n % 4 != 0 || k % 16 != 0) return NIMBUS_ERR_UNSUPPORTED;
+  if (m > (int64_t{1} << 21)) return NIMBUS_ERR_UNSUPPORTED;  // token tiles fit grid.z
+  if (m == 0) return NIMBUS_OK;
+  if (!x || !w_q || !scale || !y) return NIMBUS_ERR_INVALID;
+  if (x_stride < k || w_stride < k || y_stride < n) return NIMBUS_ERR_INVALID;
+  // Buffer offsets are 32-bit: each operand must span less than 2 GiB.
+  const int64_t x_bytes = ((m - 1) * x_stride + k) * 2;
+  const int64_t w_bytes = (static_cast<int64_t>(n) - 1) * w_stride + k;
+  if (x_bytes >= (int64_t{1} << 31) || w_bytes >= (int64_t{1} << 31)) return NIMBUS_ERR_UNSUPPORTED;
+  if (x_stride % 8 != 0 || w_stride % 16 != 0 || y_stride % 4 != 0) return NIMBUS_ERR_ALIGNMENT;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_q) | reinterpret_cast<uintptr_t>(y)) % 16 != 0 ||
+      reinterpret_cast<uintptr_t>(scale) % 8 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
+  GemmArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.sx = static_cast<int32_t>(x_stride);
+  a.w = static_cast<const int8_t*>(w_q);
+  a.sw = static_cast<int32_t>(w_stride);
+  a.x_bytes = static_cast<int32_t>(x_bytes);
+  a.w_bytes = static_cast<int32_t>(w_bytes);
+  a.scale = static_cast<const uint16_t*>(scale);
+  a.y = static_cast<uint16_t*>(y);
+  a.sy = y_stride;
+  a.M = static_cast<int32_t>(m);
+  a.N = n;
+  a.K = k;
+  gemm_split(m, n, k, &a.splits, &a.ksplit);
+  const int64_t need = a.splits > 1 ? static_cast<int64_t>(a.splits) * m * n * 4 : 0;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return NIMBUS_ERR_WORKSPACE;
+  if (need > 0 && reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
+  a.part = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == kFloat16 ? launch_gemm_dt<kFloat16>(a, s) : launch_gemm_dt<kBFloat16>(a, s);
+}

@@ -78,7 +78,7 @@ extern "C" const char* nimbus_attn_error_string(int code) {
     case NIMBUS_ERR_ALIGNMENT:
       return "a base pointer or stride breaks 16-byte vector access";
     case NIMBUS_ERR_WORKSPACE:
-      return "decode workspace missing or smaller than nimbus_paged_decode_workspace_bytes()";
+      return "workspace missing or smaller than the entry point's *_workspace_bytes()";
     default:
       return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }

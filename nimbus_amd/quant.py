@@ -1,0 +1,75 @@
+"""INT8 weight-only quantization (symmetric, per output channel).
+
+Mirrors nimbus/quant/int8.py:20-71: each weight row gets the scale
+max|row| / 127 and is stored as round(w / scale) in int8; activations stay
+in the model dtype and the scale is applied after the product
+(x @ (w_q * s)^T == (x @ w_q^T) * s). Int8Linear runs the HIP kernel
+(kernels/int8_matmul.py); the quantizer itself is host-side set-up run once
+per weight, in PyTorch on whatever device the weight lives.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from nimbus_amd.kernels.int8_matmul import int8_matmul
+
+
+def quantize_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """w: [N, K] float -> (int8 [N, K], scale [N] in w's dtype)
+    (nimbus/quant/int8.py:20-25)."""
+    wf = w.float()
+    scale = wf.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    q = torch.round(wf / scale[:, None]).clamp_(-127, 127).to(torch.int8)
+    return q, scale.to(w.dtype)
+
+
+def dequantize_weight(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """(nimbus/quant/int8.py:28-29)"""
+    return q.to(scale.dtype) * scale[:, None]
+
+
+class Int8Linear(nn.Module):
+    """nimbus/quant/int8.py:32-47 with the HIP kernel. The reference keeps a
+    PyTorch path behind use_triton=False; this module is the GPU path only,
+    so use_hip=False is refused rather than served on the CPU."""
+
+    def __init__(self, linear: nn.Linear, use_hip: bool = True):
+        super().__init__()
+        if not use_hip:
+            raise ValueError("nimbus_amd's Int8Linear is the HIP path only")
+        if linear.bias is not None:
+            raise ValueError("the decoder projections have no bias")
+        q, s = quantize_weight(linear.weight.data)
+        self.register_buffer("weight_q", q)
+        self.register_buffer("scale", s)
+        self.in_features, self.out_features = linear.in_features, linear.out_features
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return int8_matmul(x, self.weight_q, self.scale)
+
+
+QUANTIZED = ("qkv_proj", "o_proj", "gate_up_proj", "down_proj")
+
+
+@torch.no_grad()
+def quantize_model(model: nn.Module, use_hip: bool = True) -> nn.Module:
+    """Replaces the decoder projections (model.layers[i].self_attn / .mlp)
+    with Int8Linear in place (nimbus/quant/int8.py:53-65)."""
+    for layer in model.layers:
+        for parent in (layer.self_attn, layer.mlp):
+            for name in QUANTIZED:
+                lin = getattr(parent, name, None)
+                if isinstance(lin, nn.Linear):
+                    setattr(parent, name, Int8Linear(lin, use_hip))
+                    del lin
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+    return model
+
+
+def weight_bytes(model: nn.Module) -> int:
+    """(nimbus/quant/int8.py:68-71)"""
+    return sum(t.numel() * t.element_size() for t in list(model.parameters()) + list(model.buffers())
+               if t.dtype in (torch.float16, torch.bfloat16, torch.float32, torch.int8) and not t.is_meta)

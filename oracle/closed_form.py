@@ -1,4 +1,5 @@
-"""float64 NumPy brute force of the paged-attention mathematics.
+"""float64 NumPy brute force of the paged-attention mathematics (and of the
+RMSNorm and the int8 weight-only product beside it).
 
 TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
 
@@ -110,3 +111,12 @@ def rms_norm(x, weight, eps):
     xf = _np(x).astype(np.float64)
     w = _np(weight).astype(np.float64)
     return w * xf / np.sqrt(np.mean(xf * xf, axis=-1, keepdims=True) + eps)
+
+
+def int8_matmul(x, q, scale):
+    """float64 weight-only int8 product from the definition:
+    y[i, j] = sum_k x[i, k] q[j, k] * scale[j]."""
+    xf = _np(x).astype(np.float64)
+    qf = _np(q).astype(np.float64)
+    s = _np(scale).astype(np.float64)
+    return (xf @ qf.T) * s[None, :]

@@ -14,12 +14,18 @@ Each function follows one function of the reference, op for op:
                           memory (~34 GB batched)
   rms_norm                nimbus/kernels/reference.py:99-104
   add_rms_norm            nimbus/kernels/reference.py:107-112
+  quantize_weight         nimbus/quant/int8.py:20-25
+  dequantize_weight       nimbus/quant/int8.py:28-29
+  int8_matmul             the expected value of nimbus's kernel test
+                          (tests/test_quant.py:65): fp32 product of x and the
+                          int8 weights, times the fp32 scale, rounded once
 
 Pinned by tests/test_oracle.py against oracle.closed_form (float64 brute force)
 and against special cases with textbook answers (ctx=1 gives v_0; one-hot
 scores select one row of V; uniform scores average V; the slot write is a
 NumPy scatter; a constant row normalises to +-1; the residual add is NumPy's
-element-type addition).
+element-type addition; quantized weights round-trip within half a step and
+the int8 product of small integers is exact).
 """
 
 from __future__ import annotations
@@ -134,3 +140,27 @@ def add_rms_norm(x, residual, weight, eps: float):
     """
     residual = residual + x
     return rms_norm(residual, weight, eps), residual
+
+
+def quantize_weight(w):
+    """Symmetric per-output-channel int8 quantization.
+
+    Follows nimbus/quant/int8.py:20-25: scale = max|row| / 127 (rows of
+    zeros get 1e-8 / 127), q = clamp(round(w / scale), -127, 127); the scale
+    is returned in w's dtype.
+    """
+    wf = w.float()
+    scale = wf.abs().amax(dim=1).clamp_min(1e-8) / 127.0
+    q = torch.round(wf / scale[:, None]).clamp_(-127, 127).to(torch.int8)
+    return q, scale.to(w.dtype)
+
+
+def dequantize_weight(q, scale):
+    """nimbus/quant/int8.py:28-29: q in the scale's dtype times the row scale."""
+    return q.to(scale.dtype) * scale[:, None]
+
+
+def int8_matmul(x, q, scale):
+    """y = dtype(fp32(x @ q^T) * fp32(scale)): the value nimbus's own kernel
+    test expects (tests/test_quant.py:65), in x's dtype."""
+    return (x.float() @ q.float().T * scale.float()).to(x.dtype)

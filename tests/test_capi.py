@@ -24,7 +24,8 @@ def test_header_declares_the_four_launch_paths():
     names = declared_functions()
     for want in ("nimbus_write_kv", "nimbus_paged_decode", "nimbus_paged_decode_workspace_bytes",
                  "nimbus_paged_prefill", "nimbus_paged_verify", "nimbus_paged_verify_workspace_bytes",
-                 "nimbus_add_rms_norm", "nimbus_attn_abi_version",
+                 "nimbus_add_rms_norm", "nimbus_int8_matmul", "nimbus_int8_matmul_workspace_bytes",
+                 "nimbus_attn_abi_version",
                  "nimbus_attn_error_string"):
         assert want in names
 
@@ -158,3 +159,34 @@ def test_rms_norm_rejects_before_launch():
     assert f(None, 0, None, 0, None, None, 0, None, 0, 4, 16, 1e-5, 7, None) == -2  # dtype
     assert f(None, 0, None, 0, None, None, 0, None, 0, 4, 16, 1e-5, 0, None) == -1  # null x
     assert f(None, 0, None, 0, None, None, 0, None, 0, 0, 16, 1e-5, 0, None) == 0  # no rows: nothing to do
+
+
+def test_int8_matmul_rejects_before_launch():
+    """Shapes outside the kernel, null pointers and a missing split-K
+    workspace return an error code without touching memory."""
+    lib = _lib.load()
+    f = lib.nimbus_int8_matmul
+    ws = lib.nimbus_int8_matmul_workspace_bytes
+    args = lambda m, n, k, **kw: dict(x=DUMMY, xs=k, w=DUMMY, wsd=k, s=DUMMY, y=DUMMY, ys=n, m=m, n=n, k=k,
+                                      ws=None, wsb=0, dt=0, stream=None) | kw
+    call = lambda **kw: f(*kw.values())
+    assert call(**args(4, 4098, 2048)) == _lib.NIMBUS_ERR_UNSUPPORTED  # n % 4
+    assert call(**args(4, 4096, 2040)) == _lib.NIMBUS_ERR_UNSUPPORTED  # k % 16
+    assert call(**args(4, 4096, 2048, dt=5)) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert call(**args(0, 4096, 2048)) == 0
+    assert call(**args(4, 4096, 2048, x=None)) == _lib.NIMBUS_ERR_INVALID
+    assert call(**args(4, 4096, 2048, xs=2044)) == _lib.NIMBUS_ERR_INVALID  # stride below k
+    assert call(**args(4, 4096, 2048, x=DUMMY + 8)) == _lib.NIMBUS_ERR_ALIGNMENT
+    assert ws(4, 4096, 2048) > 0  # 32 channel tiles: K is split, so a workspace is needed
+    assert call(**args(4, 4096, 2048)) == _lib.NIMBUS_ERR_WORKSPACE
+    assert ws(300, 11264, 2048) == 0  # 88 x 5 tiles fill the chip: no split
+    assert ws(-1, 4, 16) == -1
+
+
+def test_int8_workspace_is_splits_times_fp32_output():
+    lib = _lib.load()
+    ws = lib.nimbus_int8_matmul_workspace_bytes
+    # 4096 channels = 32 tiles of 128, one 16-token tile: 8 splits of 14336 / 8 = 1792 -> 2048 (whole
+    # rings of 512) -> 7 splits
+    assert ws(16, 4096, 14336) == 7 * 16 * 4096 * 4
+    assert ws(1, 3072, 2048) == 4 * 1 * 3072 * 4  # 24 tiles want 11 splits; 2048 / 512 allows 4

@@ -1,0 +1,116 @@
+"""GPU: INT8 weight-only matmul against the oracle.
+
+The bar is nimbus's own (tests/test_quant.py:57-67): within atol 2e-2,
+rtol 1e-2 of fp32(x @ w_q^T) * scale rounded to the element type, on its
+matrix of M in {1, 7, 64, 300} and TinyLlama's projection shapes, in fp16.
+Added: bf16 and Llama-3-8B shapes, an exact check on small integers (pins
+the int8 -> fp16/bf16 widening bit for bit), shapes whose N and K leave
+partial tiles and steps, strided activations, and repeatability.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nimbus_amd.kernels.int8_matmul import int8_matmul, int8_matmul_workspace_bytes
+from nimbus_amd.quant import Int8Linear, quantize_weight
+from oracle import closed_form, reference
+from tests.gpu_helpers import announce
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(m, n, k, dtype, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).to(dtype)
+    q, s = quantize_weight(w)
+    x = torch.randn(m, k, generator=g, device="cuda").to(dtype)
+    return x, q, s
+
+
+@pytest.mark.parametrize("m", [1, 7, 64, 300])
+@pytest.mark.parametrize("n,k", [(3072, 2048), (2048, 5632), (11264, 2048)])
+def test_reference_matrix_fp16(m, n, k):
+    announce(f"int8_matmul fp16 m={m} n={n} k={k} ws={int8_matmul_workspace_bytes(m, n, k)}")
+    x, q, s = _case(m, n, k, torch.float16, m * 7 + n + k)
+    got = int8_matmul(x, q, s)
+    want = reference.int8_matmul(x.cpu(), q.cpu(), s.cpu())
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("m", [1, 16, 64, 130])
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336), (28672, 4096)])
+def test_llama3_shapes_bf16(m, n, k):
+    announce(f"int8_matmul bf16 m={m} n={n} k={k}")
+    x, q, s = _case(m, n, k, torch.bfloat16, m + n + k)
+    got = int8_matmul(x, q, s)
+    want = reference.int8_matmul(x.cpu(), q.cpu(), s.cpu())
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,n,k", [(5, 260, 96), (33, 4100, 1040), (64, 128, 8192), (1, 4, 16)])
+def test_small_integers_are_exact(dtype, m, n, k):
+    """Integer x and w_q with power-of-two scales: every product and partial
+    sum is exact in fp32, so the kernel must equal the float64 product
+    rounded once, whatever the tiling or K split."""
+    announce(f"int8_matmul exact {dtype} m={m} n={n} k={k}")
+    g = torch.Generator(device="cuda").manual_seed(m * n + k)
+    x = torch.randint(-3, 4, (m, k), generator=g, device="cuda").to(dtype)
+    q = torch.randint(-127, 128, (n, k), generator=g, device="cuda").to(torch.int8)
+    s = (2.0 ** -torch.randint(6, 10, (n,), generator=g, device="cuda").float()).to(dtype)
+    got = int8_matmul(x, q, s)
+    want = torch.from_numpy(closed_form.int8_matmul(x.cpu(), q.cpu(), s.cpu())).to(dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), want)
+
+
+def test_strided_rows_leading_dims_and_repeatability():
+    """x as a column slice of a wider [B, T, 3K] buffer; the same call twice
+    gives the same bits (fixed summation order)."""
+    announce("int8_matmul strided x, repeat")
+    g = torch.Generator(device="cuda").manual_seed(4)
+    wide = torch.randn(3, 5, 3 * 2048, generator=g, device="cuda").half()
+    x = wide[..., 2048:4096]
+    w = (torch.randn(3072, 2048, generator=g, device="cuda") * 0.02).half()
+    q, s = quantize_weight(w)
+    a = int8_matmul(x, q, s)
+    b = int8_matmul(x, q, s)
+    want = reference.int8_matmul(x.reshape(-1, 2048).cpu(), q.cpu(), s.cpu()).view(3, 5, 3072)
+    torch.cuda.synchronize()
+    assert a.shape == (3, 5, 3072)
+    assert torch.equal(a, b)
+    torch.testing.assert_close(a.cpu(), want, atol=2e-2, rtol=1e-2)
+
+
+def test_int8_linear_matches_dequantized_linear():
+    """Int8Linear (nimbus/quant/int8.py:32-47) against F.linear with the
+    dequantized weight, the reference module's own definition."""
+    announce("Int8Linear")
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(2048, 512, bias=False).cuda().half()
+    mod = Int8Linear(lin)
+    x = torch.randn(4, 7, 2048, device="cuda").half()
+    got = mod(x)
+    want = reference.int8_matmul(x.reshape(-1, 2048).cpu(), mod.weight_q.cpu(), mod.scale.cpu()).view(4, 7, 512)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
+    assert mod.weight_q.dtype == torch.int8 and mod.weight_q.shape == (512, 2048)
+
+
+def test_zero_rows_and_explicit_workspace():
+    announce("int8_matmul m=0, caller workspace")
+    x, q, s = _case(16, 3072, 2048, torch.float16, 2)
+    assert int8_matmul(x[:0], q, s).shape == (0, 3072)
+    need = int8_matmul_workspace_bytes(16, 3072, 2048)
+    assert need > 0  # 24 channel tiles: K is split
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    out = torch.empty(16, 3072, dtype=torch.float16, device="cuda")
+    int8_matmul(x, q, s, out=out, workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out, int8_matmul(x, q, s))
+    with pytest.raises(ValueError):
+        int8_matmul(x, q, s, workspace=ws[:need - 16])

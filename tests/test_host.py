@@ -171,3 +171,24 @@ def test_prefill_flops_formula():
     # 3 new on a prefix of 37: 3*37 + 3*4/2 pairs
     assert workloads.prefill_flops([(40, 3)], 1, 1) == 4 * (3 * 37 + 6)
     assert math.isclose(workloads.prefill_flops([(40, 3)], 2, 2), 4 * 4 * 117)
+
+
+def test_int8_matmul_wrapper_checks():
+    from nimbus_amd.kernels.int8_matmul import int8_matmul
+    from nimbus_amd.quant import Int8Linear
+
+    x = torch.zeros(2, 64, dtype=torch.float16)
+    q = torch.zeros(32, 64, dtype=torch.int8)
+    s = torch.ones(32, dtype=torch.float16)
+    with pytest.raises(ValueError):  # CPU tensors: no CPU path
+        int8_matmul(x, q, s)
+    with pytest.raises(ValueError):
+        int8_matmul(x, q.float(), s)
+    with pytest.raises(ValueError):
+        int8_matmul(x[:, :32], q, s)
+    with pytest.raises(ValueError):
+        int8_matmul(x, q, s.bfloat16())
+    with pytest.raises(NotImplementedError):
+        int8_matmul(x.float(), q, s.float())
+    with pytest.raises(ValueError):
+        Int8Linear(torch.nn.Linear(64, 32, bias=False), use_hip=False)

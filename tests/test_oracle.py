@@ -335,3 +335,73 @@ def test_planted_rms_norm_mistakes_are_caught(kind):
     want = closed_form.rms_norm(x, w, eps)
     assert np.allclose(reference.rms_norm(x, w, eps).numpy(), want, atol=1e-5)
     assert not np.allclose(bad.numpy(), want, atol=1e-3)
+
+
+# ---------------------------------------------------------------- INT8 weight-only matmul
+
+def test_quantize_roundtrip_error_is_within_half_a_step():
+    """nimbus's own check (tests/test_quant.py:7-13): |dequant(q) - w| <= s / 2."""
+    g = torch.Generator().manual_seed(0)
+    w = torch.randn(64, 300, generator=g) * torch.rand(64, 1, generator=g) * 3
+    q, s = reference.quantize_weight(w)
+    assert q.dtype == torch.int8 and int(q.abs().max()) <= 127
+    err = (reference.dequantize_weight(q, s) - w).abs()
+    assert bool((err <= s[:, None] / 2 + 1e-6).all())
+
+
+def test_quantize_maps_each_row_maximum_to_127_and_zero_rows_to_zero():
+    w = torch.tensor([[0.5, -2.0, 1.0, 0.0], [3.0, 1.5, -0.25, 0.1], [0.0, 0.0, 0.0, 0.0]])
+    q, s = reference.quantize_weight(w)
+    assert q.tolist()[0] == [32, -127, 64, 0]  # 0.5 / (2 / 127) = 31.75 -> 32
+    assert q.tolist()[1][0] == 127 and q.tolist()[2] == [0, 0, 0, 0]
+    assert np.allclose(s.numpy(), [2 / 127, 3 / 127, 1e-8 / 127])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_int8_matmul_oracle_is_exact_on_small_integers(dtype):
+    """Integer x and q with a power-of-two scale: the fp32 sum is exact, so
+    the oracle equals the float64 product rounded once to the element type."""
+    g = torch.Generator().manual_seed(3)
+    x = torch.randint(-3, 4, (9, 48), generator=g).to(dtype)
+    q = torch.randint(-127, 128, (20, 48), generator=g).to(torch.int8)
+    s = torch.full((20,), 2.0 ** -7).to(dtype) * torch.randint(1, 4, (20,), generator=g).to(dtype)
+    got = reference.int8_matmul(x, q, s)
+    want = torch.from_numpy(closed_form.int8_matmul(x, q, s)).to(dtype)
+    assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 2048), (7, 40, 96), (64, 128, 5632)])
+def test_int8_matmul_oracle_matches_float64(m, n, k):
+    """fp16 inputs, real-valued scales: within one fp16 rounding of float64,
+    and equal to the dequantized-weight product (tests/test_quant.py:16-21)."""
+    g = torch.Generator().manual_seed(m + n + k)
+    w = torch.randn(n, k, generator=g) * 0.02
+    q, s = reference.quantize_weight(w.half())
+    x = torch.randn(m, k, generator=g).half()
+    got = reference.int8_matmul(x, q, s).double().numpy()
+    want = closed_form.int8_matmul(x, q, s)
+    assert np.all(np.abs(got - want) <= 2.0 ** -10 * np.abs(want) + 1e-4)
+    deq = x.float() @ reference.dequantize_weight(q, s.float()).T
+    assert np.allclose(reference.int8_matmul(x.float(), q, s.float()).numpy(), deq.numpy(), atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("kind", ["no_scale", "scale_per_token", "transposed_weight", "x_rounded"])
+def test_planted_int8_matmul_mistakes_are_caught(kind):
+    """The float64 check and the reference's bar (atol 2e-2, rtol 1e-2) reject
+    plausible slips in the int8 product."""
+    g = torch.Generator().manual_seed(8)
+    n = k = 64
+    w = torch.randn(n, k, generator=g) * 0.05
+    q, s = reference.quantize_weight(w)
+    x = torch.randn(n, k, generator=g) * 2
+    want = closed_form.int8_matmul(x, q, s)
+    if kind == "no_scale":
+        bad = x @ q.float().T
+    elif kind == "scale_per_token":
+        bad = (x @ q.float().T) * s[:, None]
+    elif kind == "transposed_weight":
+        bad = (x @ q.float()) * s
+    else:
+        bad = (torch.round(x) @ q.float().T) * s
+    assert max_violation(reference.int8_matmul(x, q, s), want, 2e-2, 1e-2) <= 0
+    assert max_violation(bad, want, 2e-2, 1e-2) > 0
