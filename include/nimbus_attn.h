@@ -4,8 +4,9 @@
  * libnimbus_attn.so replaces the GPU side of Nimbus's attention hot path:
  * the KV slot write, paged decode attention, causal varlen paged prefill
  * attention (with a verify form for uniform short query runs), the fused
- * residual add + RMSNorm on either side of it, and the INT8 weight-only
- * matmul of the quantized projections. Every entry point
+ * residual add + RMSNorm on either side of it, the INT8 weight-only
+ * matmul of the quantized projections, and the rotary embedding and SiLU
+ * gate of the decoder layer around them. Every entry point
  * takes plain device pointers, element strides
  * (not bytes), sizes, a dtype code and an opaque hipStream_t; none allocates,
  * frees, synchronises or reads device memory on the host, so each call can be
@@ -28,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 5
+#define NIMBUS_ATTN_ABI_VERSION 6
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -218,6 +219,45 @@ int64_t nimbus_int8_matmul_workspace_bytes(int64_t m, int32_t n, int32_t k);
 int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w_q, int64_t w_stride, const void* scale,
                        void* y, int64_t y_stride, int64_t m, int32_t n, int32_t k, void* workspace,
                        int64_t workspace_bytes, int32_t dtype, void* stream);
+
+/*
+ * Rotary position embedding, in place. Replaces Rotary.forward
+ * (nimbus/model/llama.py:37-57) on the q and k heads of the fused qkv
+ * projection: token t (row stride x_stride elements) holds num_heads heads
+ * of head_dim; each head's pairs (i, i + head_dim/2) rotate by the
+ * positions[t] row of the fp32 cos / sin tables (row stride table_stride),
+ * with every multiply and the add rounded to dtype as the reference's ops
+ * are. Tokens whose position is outside [0, max_position) are left as is.
+ * head_dim a multiple of 16; x 16-byte aligned, x_stride a multiple of 8.
+ */
+int nimbus_rope(void* x, int64_t x_stride, int64_t num_tokens, int32_t num_heads, int32_t head_dim,
+                const int64_t* positions, const float* cos_table, const float* sin_table, int64_t table_stride,
+                int32_t max_position, int32_t dtype, void* stream);
+
+/*
+ * SiLU-gated product of the MLP. Replaces F.silu(gate) * up
+ * (nimbus/model/llama.py:100-103): row r of x holds [gate | up] (2 * cols
+ * elements); out[r] = dtype(dtype(silu(gate)) * up). cols a multiple of 8;
+ * x and out 16-byte aligned, strides multiples of 8.
+ */
+int nimbus_silu_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride, int64_t rows, int32_t cols,
+                    int32_t dtype, void* stream);
+
+/*
+ * One step of the on-device greedy chain. Replaces the loop body of
+ * DecodeGraphs.greedy_chain (nimbus/cuda_graph.py:104-115): for each row r
+ * < rows, tok = argmax(logits[r, :vocab]) (first index among equal maxima)
+ * becomes input_ids[r]; for rows with active[r] != 0 it is also recorded at
+ * tokens[r, context_lens[r] - ctx_start[r]] (when that is < max_steps), and
+ * positions[r], context_lens[r] advance by one and slots[r] becomes the
+ * cache slot of the new position through block_tables[r] (scratch_slot past
+ * the table's width). Inactive rows (padding) only take the token.
+ */
+int nimbus_greedy_step(const float* logits, int64_t logits_stride, int32_t rows, int32_t vocab, int64_t* input_ids,
+                       int64_t* positions, int32_t* context_lens, int64_t* slots, const int32_t* block_tables,
+                       int64_t bt_stride, int32_t bt_width, int32_t block_size, const int32_t* active,
+                       const int32_t* ctx_start, int64_t* tokens, int32_t max_steps, int64_t scratch_slot,
+                       void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,0 +1,292 @@
+// Rotary embedding and SiLU-gated product of the Llama decoder for gfx950.
+//
+// nimbus_rope replaces Rotary.forward (nimbus/model/llama.py:37-57): for
+// token t at position p, every head's pairs (i, i + D/2) become
+//   out_i       = x_i c_i - x_{i+D/2} s_i
+//   out_{i+D/2} = x_{i+D/2} c_{i+D/2} + x_i s_{i+D/2}
+// with c = dtype(cos[p]), s = dtype(sin[p]) (the fp32 tables of llama.py:
+// 43-47 cast to the model dtype). Each product and the sum are rounded to
+// the model dtype, as the reference's separate multiplies and add are, so
+// the result is the reference's bit for bit. It runs in place on the q and k
+// parts of the fused qkv projection (one launch for both).
+//
+// nimbus_silu_mul replaces MLP.forward's F.silu(gate) * up
+// (nimbus/model/llama.py:93-103): silu in fp32 rounded to the model dtype,
+// then the product rounded again.
+//
+// nimbus_greedy_step is one link of DecodeGraphs.greedy_chain
+// (nimbus/cuda_graph.py:92-116) on the device: per row, the argmax of the
+// logits (first index among equal maxima, as torch.argmax) becomes the next
+// input token and is recorded, and the row's position, context length and
+// cache slot advance.
+#include "common.h"
+#include "nimbus_attn_internal.h"
+
+namespace nimbus {
+
+struct RopeArgs {
+  uint16_t* x;
+  int64_t sx;        // elements between tokens
+  const int64_t* pos;
+  const float* cos;
+  const float* sin;
+  int64_t st;        // elements between table rows
+  int32_t tokens, heads, d, max_pos;
+};
+
+template <int DT>
+__device__ __forceinline__ float rnd(float v) {
+  return Elem<DT>::to_f32(Elem<DT>::from_f32(v));
+}
+
+// One thread per (token, head, 8 consecutive i < D/2): 16-byte loads of x at
+// i and i + D/2.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+  // The products are rounded before the add; a fused multiply-add would skip
+  // that rounding (hipcc contracts by default).
+#pragma clang fp contract(off)
+  const int half = a.d / 2;
+  const int per_head = half / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(a.tokens) * a.heads * per_head;
+  if (idx >= total) return;
+  const int c = static_cast<int>(idx % per_head);
+  const int h = static_cast<int>((idx / per_head) % a.heads);
+  const int64_t t = idx / (static_cast<int64_t>(per_head) * a.heads);
+  const int64_t p = a.pos[t];
+  if (p < 0 || p >= a.max_pos) return;  // no table row: left as is
+  const int i0 = 8 * c;
+  uint16_t* row = a.x + t * a.sx + static_cast<int64_t>(h) * a.d;
+  const u32x4 lo = *reinterpret_cast<const u32x4*>(row + i0);
+  const u32x4 hi = *reinterpret_cast<const u32x4*>(row + half + i0);
+  const float* cr = a.cos + p * a.st;
+  const float* sr = a.sin + p * a.st;
+  u32x4 olo, ohi;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint16_t out_lo[2], out_hi[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const int i = i0 + 2 * e + b;
+      const float xl = Elem<DT>::to_f32(static_cast<uint16_t>(lo[e] >> (16 * b)));
+      const float xh = Elem<DT>::to_f32(static_cast<uint16_t>(hi[e] >> (16 * b)));
+      const float cl = rnd<DT>(cr[i]), sl = rnd<DT>(sr[i]);
+      const float ch = rnd<DT>(cr[i + half]), sh = rnd<DT>(sr[i + half]);
+      // x * cos + rotate_half(x) * sin, rotate_half(x) = cat(-x_hi, x_lo)
+      out_lo[b] = Elem<DT>::from_f32(rnd<DT>(xl * cl) + rnd<DT>(-xh * sl));
+      out_hi[b] = Elem<DT>::from_f32(rnd<DT>(xh * ch) + rnd<DT>(xl * sh));
+    }
+    olo[e] = pack2(out_lo[0], out_lo[1]);
+    ohi[e] = pack2(out_hi[0], out_hi[1]);
+  }
+  *reinterpret_cast<u32x4*>(row + i0) = olo;
+  *reinterpret_cast<u32x4*>(row + half + i0) = ohi;
+}
+
+struct SiluArgs {
+  const uint16_t* x;
+  int64_t sx;
+  uint16_t* out;
+  int64_t so;
+  int32_t rows, cols;
+};
+
+// One thread per 8 consecutive outputs of a row.
+template <int DT>
+__global__ __launch_bounds__(256) void silu_mul_kernel(SiluArgs a) {
+  const int per_row = a.cols / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= static_cast<int64_t>(a.rows) * per_row) return;
+  const int64_t r = idx / per_row;
+  const int c = static_cast<int>(idx % per_row) * 8;
+  const uint16_t* xr = a.x + r * a.sx;
+  const u32x4 g = *reinterpret_cast<const u32x4*>(xr + c);
+  const u32x4 u = *reinterpret_cast<const u32x4*>(xr + a.cols + c);
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    uint16_t v[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const float gv = Elem<DT>::to_f32(static_cast<uint16_t>(g[e] >> (16 * b)));
+      const float uv = Elem<DT>::to_f32(static_cast<uint16_t>(u[e] >> (16 * b)));
+      const float s = rnd<DT>(gv / (1.f + expf(-gv)));
+      v[b] = Elem<DT>::from_f32(s * uv);
+    }
+    o[e] = pack2(v[0], v[1]);
+  }
+  *reinterpret_cast<u32x4*>(a.out + r * a.so + c) = o;
+}
+
+struct GreedyArgs {
+  const float* logits;
+  int64_t sl;
+  int32_t rows, vocab;
+  int64_t* input_ids;
+  int64_t* positions;
+  int32_t* ctx;
+  int64_t* slots;
+  const int32_t* tables;
+  int64_t bt_stride;
+  int32_t bt_width, block_size;
+  const int32_t* active;
+  const int32_t* ctx_start;
+  int64_t* tokens;
+  int32_t max_steps;
+  int64_t scratch_slot;
+};
+
+// (value, index) order of the argmax: larger value, then smaller index.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+// One 256-thread workgroup per row.
+__global__ __launch_bounds__(256) void greedy_step_kernel(GreedyArgs a) {
+  const int row = blockIdx.x;
+  const float* lr = a.logits + static_cast<int64_t>(row) * a.sl;
+  float bv = -INFINITY;
+  int bi = a.vocab;
+  for (int i = threadIdx.x; i < a.vocab; i += 256) {
+    const float v = lr[i];
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, 64);
+    const int oi = __shfl_xor(bi, off, 64);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  const int wave = threadIdx.x / 64;
+  if (threadIdx.x % 64 == 0) {
+    sv[wave] = bv;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < 4; ++w) {
+    if (better(sv[w], si[w], bv, bi)) {
+      bv = sv[w];
+      bi = si[w];
+    }
+  }
+  const int64_t tok = bi < a.vocab ? bi : 0;  // a row of NaNs picks token 0
+  a.input_ids[row] = tok;
+  if (!a.active[row]) return;
+  const int k = a.ctx[row] - a.ctx_start[row];
+  if (k >= 0 && k < a.max_steps) a.tokens[static_cast<int64_t>(row) * a.max_steps + k] = tok;
+  const int64_t p = a.positions[row] + 1;
+  a.positions[row] = p;
+  a.ctx[row] += 1;
+  const int64_t page = p / a.block_size;
+  a.slots[row] = page < a.bt_width
+                     ? static_cast<int64_t>(a.tables[row * a.bt_stride + page]) * a.block_size + p % a.block_size
+                     : a.scratch_slot;
+}
+
+}  // namespace nimbus
+
+using namespace nimbus;
+
+extern "C" int nimbus_greedy_step(const float* logits, int64_t logits_stride, int32_t rows, int32_t vocab,
+                                  int64_t* input_ids, int64_t* positions, int32_t* context_lens, int64_t* slots,
+                                  const int32_t* block_tables, int64_t bt_stride, int32_t bt_width,
+                                  int32_t block_size, const int32_t* active, const int32_t* ctx_start,
+                                  int64_t* tokens, int32_t max_steps, int64_t scratch_slot, void* stream) {
+  if (rows < 0 || vocab <= 0 || block_size <= 0 || bt_width <= 0 || max_steps < 0) return NIMBUS_ERR_INVALID;
+  if (rows == 0) return NIMBUS_OK;
+  if (!logits || !input_ids || !positions || !context_lens || !slots || !block_tables || !active || !ctx_start ||
+      (max_steps > 0 && !tokens))
+    return NIMBUS_ERR_INVALID;
+  if (logits_stride < vocab || bt_stride < bt_width) return NIMBUS_ERR_INVALID;
+  GreedyArgs a;
+  a.logits = logits;
+  a.sl = logits_stride;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.input_ids = input_ids;
+  a.positions = positions;
+  a.ctx = context_lens;
+  a.slots = slots;
+  a.tables = block_tables;
+  a.bt_stride = bt_stride;
+  a.bt_width = bt_width;
+  a.block_size = block_size;
+  a.active = active;
+  a.ctx_start = ctx_start;
+  a.tokens = tokens;
+  a.max_steps = max_steps;
+  a.scratch_slot = scratch_slot;
+  hipLaunchKernelGGL(greedy_step_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int nimbus_rope(void* x, int64_t x_stride, int64_t num_tokens, int32_t num_heads, int32_t head_dim,
+                           const int64_t* positions, const float* cos_table, const float* sin_table,
+                           int64_t table_stride, int32_t max_position, int32_t dtype, void* stream) {
+  if (num_tokens < 0 || num_heads <= 0 || head_dim <= 0 || max_position <= 0) return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (head_dim % 16 != 0 || num_tokens > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return NIMBUS_OK;
+  if (!x || !positions || !cos_table || !sin_table) return NIMBUS_ERR_INVALID;
+  if (x_stride < static_cast<int64_t>(num_heads) * head_dim || table_stride < head_dim) return NIMBUS_ERR_INVALID;
+  if (x_stride % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
+  RopeArgs a;
+  a.x = static_cast<uint16_t*>(x);
+  a.sx = x_stride;
+  a.pos = positions;
+  a.cos = cos_table;
+  a.sin = sin_table;
+  a.st = table_stride;
+  a.tokens = static_cast<int32_t>(num_tokens);
+  a.heads = num_heads;
+  a.d = head_dim;
+  a.max_pos = max_position;
+  const int64_t threads = num_tokens * num_heads * (head_dim / 16);
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == kFloat16) {
+    hipLaunchKernelGGL((rope_kernel<kFloat16>), grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((rope_kernel<kBFloat16>), grid, dim3(256), 0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int nimbus_silu_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride, int64_t rows,
+                               int32_t cols, int32_t dtype, void* stream) {
+  if (rows < 0 || cols <= 0) return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (cols % 8 != 0 || rows > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
+  if (rows == 0) return NIMBUS_OK;
+  if (!x || !out) return NIMBUS_ERR_INVALID;
+  if (x_stride < 2 * static_cast<int64_t>(cols) || out_stride < cols) return NIMBUS_ERR_INVALID;
+  if ((x_stride | out_stride) % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
+  SiluArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.sx = x_stride;
+  a.out = static_cast<uint16_t*>(out);
+  a.so = out_stride;
+  a.rows = static_cast<int32_t>(rows);
+  a.cols = cols;
+  const int64_t threads = rows * (cols / 8);
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == kFloat16) {
+    hipLaunchKernelGGL((silu_mul_kernel<kFloat16>), grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((silu_mul_kernel<kBFloat16>), grid, dim3(256), 0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}

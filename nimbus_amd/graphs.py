@@ -1,5 +1,13 @@
-"""Decode and speculative-verify attention replayed from hipGraphs at padded
-batch sizes.
+"""Decode steps and speculative-verify attention replayed from hipGraphs at
+padded batch sizes.
+
+DecodeGraphs replays the whole model's decode step (nimbus/cuda_graph.py:
+28-144): embedding, every layer, final norm and logits, captured once per
+padded batch size; greedy_chain runs many greedy steps without returning
+to the host, each one a replay of the step graph and of a one-kernel graph
+that picks the tokens and advances positions, context lengths and slots on
+the device. DecodeAttentionGraphs and VerifyAttentionGraphs replay the
+attention layer alone.
 
 Follows the capture contract of Nimbus's DecodeGraphs (nimbus/cuda_graph.py:
 38-79 and 118-144), restricted to the attention layer (the slot write plus
@@ -28,6 +36,7 @@ import bisect
 
 import torch
 
+from nimbus_amd.kernels.elementwise import greedy_step
 from nimbus_amd.kernels.paged_attention import (PAGE, decode_workspace_bytes, new_decode_workspace,
                                                 verify_workspace_bytes)
 from nimbus_amd.kernels.prefill_attention import verify_queries
@@ -256,3 +265,153 @@ class VerifyAttentionGraphs:
         """One verification step's attention: returns [n * q, H, D]."""
         n = context_lens.shape[0]
         return self.replay(self.load(q, k, v, slot_mapping, context_lens, block_tables))[:n * self.q_len]
+
+
+class DecodeGraphs:
+    """Whole decode steps of `model` replayed from hipGraphs.
+
+    Follows nimbus/cuda_graph.py:28-144: static input buffers sized for
+    max_batch, a step's batch padded up to the nearest captured size
+    (PADDED_SIZES below max_batch, then max_batch), padding rows at position
+    0 with context 1 writing and reading the scratch block, and the decode
+    grid pinned by max_model_len so one graph per size serves every mix of
+    context lengths. The model's attention backend gets a decode workspace
+    of its own (sized for max_batch and max_model_len) unless it has one.
+
+    greedy_chain keeps every step on the device: after each replay of the
+    step graph, a second captured graph (one nimbus_greedy_step kernel)
+    takes each row's argmax as its next token, records it, and advances the
+    real rows' positions, context lengths and slots; the host only reads the
+    recorded tokens at the end. A chain is at most max_chain steps.
+    """
+
+    def __init__(self, model, kv_layers, block_size: int, max_model_len: int, max_batch: int, scratch_block: int,
+                 num_kv_heads: int, device, max_chain: int = 256):
+        self.model = model
+        self.kv_layers = kv_layers
+        self.block_size = block_size
+        self.max_model_len = max_model_len
+        self.scratch_block = scratch_block
+        self.scratch_slot = scratch_block * block_size
+        self.sizes = [b for b in PADDED_SIZES if b < max_batch] + [max_batch]
+        self.max_batch = max_batch
+        self.max_chain = max_chain
+        self.kv_heads = num_kv_heads
+        self.device = device
+        width = -(-max_model_len // block_size)
+        i64, i32 = torch.int64, torch.int32
+        self.input_ids = torch.zeros(max_batch, dtype=i64, device=device)
+        self.positions = torch.zeros(max_batch, dtype=i64, device=device)
+        self.slots = torch.full((max_batch,), self.scratch_slot, dtype=i64, device=device)
+        self.ctx = torch.ones(max_batch, dtype=i32, device=device)
+        self.tables = torch.full((max_batch, width), scratch_block, dtype=i32, device=device)
+        self.active = torch.zeros(max_batch, dtype=i32, device=device)
+        self.ctx_start = torch.ones(max_batch, dtype=i32, device=device)
+        self.tokens = torch.zeros(max_batch, max_chain, dtype=i64, device=device)
+        # Pinned staging for _load (allocated pinned, never registered).
+        self._host = torch.empty((4, max_batch), dtype=i64, pin_memory=True)
+        self._host_tables = torch.empty((max_batch, width), dtype=i32, pin_memory=True)
+        self._staged = None  # event after the last staged copies: the pinned rows are reused only after it
+        backend = model.backend
+        if backend.decode_workspace is None:
+            cfg = model.cfg
+            backend.decode_workspace = new_decode_workspace(
+                decode_workspace_bytes(max_batch, cfg.num_heads, cfg.head_dim, max_model_len), device)
+        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata, torch.cuda.CUDAGraph]] = {}
+
+    def _meta(self, b: int) -> AttnMetadata:
+        empty = torch.zeros(0, dtype=torch.int32, device=self.device)
+        return AttnMetadata(
+            slot_mapping=self.slots[:b], num_prefill_tokens=0,
+            prefill_query_start=torch.zeros(1, dtype=torch.int32, device=self.device),
+            prefill_context_lens=empty, prefill_block_tables=empty.view(0, 1),
+            decode_context_lens=self.ctx[:b], decode_block_tables=self.tables[:b],
+            max_decode_context=self.max_model_len, prefill_query_start_host=[0], prefill_context_lens_host=[])
+
+    def _step(self, b: int, meta: AttnMetadata) -> torch.Tensor:
+        return self.model.logits(self.model(self.input_ids[:b], self.positions[:b], self.kv_layers, meta))
+
+    def _advance(self, b: int, logits: torch.Tensor) -> None:
+        greedy_step(logits, self.input_ids, self.positions, self.ctx, self.slots, self.tables, self.block_size,
+                    self.active, self.ctx_start, self.tokens, self.scratch_slot)
+
+    @torch.inference_mode()
+    def capture(self) -> None:
+        pool = torch.cuda.graph_pool_handle()
+        for b in reversed(self.sizes):  # largest first, so the pool is sized once
+            meta = self._meta(b)
+            for _ in range(2):
+                self._step(b, meta)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                logits = self._step(b, meta)
+            adv = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(adv, pool=pool):
+                self._advance(b, logits)
+            self.graphs[b] = (g, logits, meta, adv)  # meta's tensors must outlive the graph
+        torch.cuda.synchronize()
+
+    def can_run(self, batch) -> bool:
+        """(sequence, tokens) pairs that are all plain decodes (cuda_graph.py:83-85)."""
+        return 0 < len(batch) <= self.max_batch and all(
+            n == 1 and s.num_computed > 0 and s.num_computed + 1 == len(s) for s, n in batch)
+
+    @torch.inference_mode()
+    def run(self, seqs) -> torch.Tensor:
+        """One decode step for seqs; returns their logits [len(seqs), vocab]
+        (fp32, a view of the graph's output, valid until the next replay)."""
+        g, logits, _, _ = self.graphs[self._load(seqs)]
+        g.replay()
+        return logits[:len(seqs)]
+
+    @torch.inference_mode()
+    def greedy_chain(self, seqs, steps: int) -> torch.Tensor:
+        """`steps` greedy decode steps without returning to the host; returns
+        the chosen tokens [len(seqs), steps]. Every block table must already
+        cover `steps` more tokens (cuda_graph.py:92-99)."""
+        if not 0 < steps <= self.max_chain:
+            raise ValueError(f"steps must be in 1..{self.max_chain}")
+        n = len(seqs)
+        g, _, _, adv = self.graphs[self._load(seqs)]
+        for _ in range(steps):
+            g.replay()
+            adv.replay()
+        return self.tokens[:n, :steps].clone()
+
+    def _load(self, seqs) -> int:
+        """Copies seqs' next-token inputs into the static buffers (through
+        pinned staging, cuda_graph.py:118-144); returns the captured size."""
+        n = len(seqs)
+        if not 0 < n <= self.max_batch:
+            raise ValueError(f"batch {n} outside 1..{self.max_batch}")
+        b = self.sizes[bisect.bisect_left(self.sizes, n)]
+        bs = self.block_size
+        h, ht = self._host, self._host_tables
+        if self._staged is not None:
+            self._staged.synchronize()  # the previous call's copies have read the pinned rows
+        for i, s in enumerate(seqs):
+            p = s.num_computed
+            if len(s.block_table) > ht.shape[1]:
+                raise ValueError("a block table is wider than max_model_len allows")
+            h[0, i] = s.token_ids[p]
+            h[1, i] = p
+            h[2, i] = s.block_table[p // bs] * bs + p % bs
+            h[3, i] = p + 1
+            ht[i, :len(s.block_table)] = torch.as_tensor(s.block_table, dtype=torch.int32)
+        h[0, n:b] = 0
+        h[1, n:b] = 0
+        h[2, n:b] = self.scratch_slot
+        h[3, n:b] = 1
+        ht[n:b, 0] = self.scratch_block
+        self.input_ids[:b].copy_(h[0, :b], non_blocking=True)
+        self.positions[:b].copy_(h[1, :b], non_blocking=True)
+        self.slots[:b].copy_(h[2, :b], non_blocking=True)
+        self.ctx[:b].copy_(h[3, :b], non_blocking=True)
+        self.tables[:b].copy_(ht[:b], non_blocking=True)
+        self._staged = torch.cuda.Event()
+        self._staged.record()
+        self.ctx_start[:b].copy_(self.ctx[:b])
+        self.active[:n].fill_(1)
+        self.active[n:b].fill_(0)
+        return b

@@ -1,0 +1,255 @@
+"""GPU: the Llama decoder on this build's kernels, its whole-step decode
+graphs and the on-device greedy chain.
+
+- The model (fp16 and bf16, random weights) against oracle/model.py (the
+  CPU fp32 restatement of nimbus/model/llama.py, itself pinned to HF's
+  Llama): a mixed prefill step of three prompts, then greedy decode steps,
+  logits within a bar set by the element type.
+- Decode steps replayed from DecodeGraphs against the eager model
+  (nimbus's test_cuda_graph_decode_matches_eager, test_kernels.py:118-142):
+  the same greedy tokens, logits within rounding, batches padded to captured
+  sizes; replays are repeatable bit for bit.
+- greedy_chain against step-by-step graph runs with host argmax: identical
+  tokens (the same kernels), and every graph replay equals the eager call.
+- The INT8-quantized model stays close to the unquantized one
+  (nimbus's test_quantized_tiny_model_stays_close: cosine > 0.99).
+- The rotary, SiLU and greedy-step kernels against torch.
+"""
+
+from __future__ import annotations
+
+import random
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from nimbus_amd.graphs import DecodeGraphs
+from nimbus_amd.kernels.elementwise import greedy_step, rope_, silu_mul
+from nimbus_amd.model.attention import AttnMetadata
+from nimbus_amd.model.config import ModelConfig
+from nimbus_amd.model.llama import build_model
+from nimbus_amd.model.runner import Sequence, prepare
+from nimbus_amd.quant import quantize_model
+from oracle import model as omodel
+from tests.gpu_helpers import announce
+
+pytestmark = pytest.mark.gpu
+
+CFG = ModelConfig(vocab_size=1000, hidden_size=256, intermediate_size=512, num_layers=2, num_heads=4,
+                  num_kv_heads=2, head_dim=64, rms_norm_eps=1e-5, rope_theta=10000.0, max_position=1024)
+BS = 16
+
+
+def _setup(dtype, prompt_lens, num_blocks=96, seed=0, cfg=CFG):
+    model = build_model(cfg, dtype, "cuda", seed, max_position=cfg.max_position)
+    shape = (num_blocks + 1, BS, cfg.num_kv_heads, cfg.head_dim)  # + the scratch block (num_blocks)
+    caches = [(torch.zeros(shape, dtype=dtype, device="cuda"), torch.zeros(shape, dtype=dtype, device="cuda"))
+              for _ in range(cfg.num_layers)]
+    rng = random.Random(seed)
+    pool = rng.sample(range(num_blocks), num_blocks)
+    seqs = []
+    for i, n in enumerate(prompt_lens):
+        ids = [rng.randrange(1, cfg.vocab_size) for _ in range(n)]
+        s = Sequence(i, ids)
+        s.block_table = [pool.pop() for _ in range(-(-(n + 24) // BS))]  # room for 24 more tokens
+        seqs.append(s)
+    return model, caches, seqs
+
+
+def _cpu_meta(meta: AttnMetadata) -> AttnMetadata:
+    c = lambda t: t.cpu()  # noqa: E731
+    return AttnMetadata(c(meta.slot_mapping), meta.num_prefill_tokens, c(meta.prefill_query_start),
+                        c(meta.prefill_context_lens), c(meta.prefill_block_tables), c(meta.decode_context_lens),
+                        c(meta.decode_block_tables), meta.max_decode_context, meta.prefill_query_start_host,
+                        meta.prefill_context_lens_host)
+
+
+def _eager_step(model, caches, batch):
+    step = prepare(batch, BS, "cuda")
+    logits = model.logits(model(step.input_ids, step.positions, caches, step.meta))
+    return step, logits[step.sample_rows]
+
+
+@pytest.mark.parametrize("dtype,atol", [(torch.float16, 2e-2), (torch.bfloat16, 6e-2)])
+def test_model_matches_oracle_prefill_then_decode(dtype, atol):
+    announce(f"model vs oracle {dtype}")
+    model, caches, seqs = _setup(dtype, [5, 17, 40])
+    w = {k: v.float().cpu() for k, v in model.state_dict().items()}
+    ocaches = [(torch.zeros(kc.shape), torch.zeros(vc.shape)) for kc, vc in caches]
+    batch = [(s, len(s)) for s in seqs]
+    for step_i in range(4):
+        step, got = _eager_step(model, caches, batch)
+        meta = _cpu_meta(step.meta)
+        hid = omodel.forward(w, CFG, step.input_ids.cpu(), step.positions.cpu(), ocaches, meta, CFG.max_position)
+        want = omodel.logits(w, hid)[step.sample_rows.cpu()]
+        got = got.cpu()
+        err = (got - want).abs().max().item()
+        announce(f"  step {step_i}: max |logit error| {err:.2e} (logit scale {want.abs().max().item():.2f})")
+        assert err <= atol * max(1.0, want.abs().max().item()), err
+        for s, tok in zip(seqs, got.argmax(-1).tolist()):  # same inputs for both next step
+            s.num_computed = len(s)
+            s.append(tok)
+        batch = [(s, 1) for s in seqs]
+
+
+def _prefill(model, caches, seqs):
+    _, logits = _eager_step(model, caches, [(s, len(s)) for s in seqs])
+    for s, tok in zip(seqs, logits.argmax(-1).tolist()):
+        s.num_computed = len(s)
+        s.append(tok)
+
+
+def _clone_seqs(seqs):
+    out = []
+    for s in seqs:
+        c = Sequence(s.seq_id, list(s.prompt_ids), list(s.block_table), s.num_computed)
+        c.token_ids, c.output_ids = list(s.token_ids), list(s.output_ids)
+        out.append(c)
+    return out
+
+
+def _clone_caches(caches):
+    return [(kc.clone(), vc.clone()) for kc, vc in caches]
+
+
+@pytest.mark.parametrize("n,dtype", [(5, torch.float16), (3, torch.bfloat16), (16, torch.float16)])
+def test_decode_graphs_match_eager(n, dtype):
+    announce(f"decode graphs n={n} {dtype}")
+    model, caches, seqs = _setup(dtype, [3 + 7 * i for i in range(n)], num_blocks=160, seed=n)
+    _prefill(model, caches, seqs)
+    g_seqs, e_seqs = _clone_seqs(seqs), _clone_seqs(seqs)
+    g_caches, e_caches = _clone_caches(caches), _clone_caches(caches)
+    graphs = DecodeGraphs(model, g_caches, BS, max_model_len=512, max_batch=16, scratch_block=160,
+                          num_kv_heads=CFG.num_kv_heads, device="cuda")
+    graphs.capture()
+    for step_i in range(5):
+        assert graphs.can_run([(s, 1) for s in g_seqs])
+        got = graphs.run(g_seqs).clone()
+        _, want = _eager_step(model, e_caches, [(s, 1) for s in e_seqs])
+        torch.testing.assert_close(got, want, atol=1e-2, rtol=1e-2)
+        g_tok, e_tok = got.argmax(-1).tolist(), want.argmax(-1).tolist()
+        assert g_tok == e_tok, (step_i, g_tok, e_tok)
+        for s, t in zip(g_seqs, g_tok):
+            s.num_computed = len(s)
+            s.append(t)
+        for s, t in zip(e_seqs, e_tok):
+            s.num_computed = len(s)
+            s.append(t)
+
+
+def test_greedy_chain_matches_stepwise_runs():
+    """The chain's on-device argmax and state advance equal host-side
+    argmax + _load between single-step replays, token for token."""
+    announce("greedy chain")
+    model, caches, seqs = _setup(torch.float16, [9, 30, 4, 51, 17], num_blocks=160, seed=11)
+    _prefill(model, caches, seqs)
+    a_seqs, b_seqs = _clone_seqs(seqs), _clone_seqs(seqs)
+    a_caches, b_caches = _clone_caches(caches), _clone_caches(caches)
+    steps = 12
+    ga = DecodeGraphs(model, a_caches, BS, 512, 8, 160, CFG.num_kv_heads, "cuda", max_chain=32)
+    ga.capture()
+    chain = ga.greedy_chain(a_seqs, steps).cpu()
+    gb = DecodeGraphs(model, b_caches, BS, 512, 8, 160, CFG.num_kv_heads, "cuda")
+    gb.capture()
+    for k in range(steps):
+        toks = gb.run(b_seqs).argmax(-1).tolist()
+        assert toks == chain[:, k].tolist(), k
+        for s, t in zip(b_seqs, toks):
+            s.num_computed = len(s)
+            s.append(t)
+    # both graph paths wrote the same K/V into their caches
+    for (ka, va), (kb, vb) in zip(a_caches, b_caches):
+        assert torch.equal(ka[:160], kb[:160]) and torch.equal(va[:160], vb[:160])
+
+
+def test_int8_model_stays_close():
+    announce("int8 model vs fp16")
+    model, caches, seqs = _setup(torch.float16, [12, 33, 7], seed=5)
+    q_model, _, _ = _setup(torch.float16, [12, 33, 7], seed=5)
+    quantize_model(q_model)
+    assert q_model.layers[0].mlp.down_proj.weight_q.dtype == torch.int8
+    q_caches = _clone_caches(caches)
+    batch = [(s, len(s)) for s in seqs]
+    q_seqs = _clone_seqs(seqs)
+    q_batch = [(s, len(s)) for s in q_seqs]
+    for _ in range(4):
+        _, ref = _eager_step(model, caches, batch)
+        _, got = _eager_step(q_model, q_caches, q_batch)
+        cos = F.cosine_similarity(ref, got, dim=-1)
+        assert cos.min().item() > 0.99, cos
+        toks = ref.argmax(-1).tolist()  # feed both the unquantized model's tokens
+        for s, t in zip(seqs, toks):
+            s.num_computed = len(s)
+            s.append(t)
+        for s, t in zip(q_seqs, toks):
+            s.num_computed = len(s)
+            s.append(t)
+        batch = [(s, 1) for s in seqs]
+        q_batch = [(s, 1) for s in q_seqs]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("heads,d", [(40, 128), (6, 64)])
+def test_rope_kernel_is_the_reference_arithmetic(dtype, heads, d):
+    """x * cos + rotate_half(x) * sin in the element type, tables cast from
+    fp32 (nimbus/model/llama.py:49-58), bit for bit; a position outside the
+    table leaves its row alone."""
+    announce(f"rope {dtype} heads={heads} d={d}")
+    g = torch.Generator(device="cuda").manual_seed(d)
+    t = 37
+    x = torch.randn(t, heads * d + 3 * 8, generator=g, device="cuda").to(dtype)  # row wider than the heads
+    pos = torch.randint(0, 500, (t,), generator=g, device="cuda")
+    pos[5] = 600  # past the table
+    ang = torch.arange(512, device="cuda", dtype=torch.float32)[:, None] * torch.rand(d // 2, generator=g,
+                                                                                      device="cuda")[None]
+    ang = torch.cat([ang, ang], -1)
+    cos, sin = ang.cos(), ang.sin()
+    got = rope_(x.clone(), heads, d, pos, cos, sin)
+    xh = x[:, :heads * d].view(t, heads, d)
+    pc = pos.clamp(max=511)
+    c, s = cos[pc].to(dtype)[:, None, :], sin[pc].to(dtype)[:, None, :]
+    rot = torch.cat([-xh[..., d // 2:], xh[..., :d // 2]], -1)
+    want = (xh * c + rot * s).view(t, heads * d)
+    keep = torch.ones(t, dtype=torch.bool, device="cuda")
+    keep[5] = False
+    assert torch.equal(got[keep, :heads * d], want[keep])
+    assert torch.equal(got[5], x[5]) and torch.equal(got[:, heads * d:], x[:, heads * d:])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_silu_mul_kernel(dtype):
+    announce(f"silu_mul {dtype}")
+    g = torch.Generator(device="cuda").manual_seed(1)
+    x = (torch.randn(19, 2 * 1376, generator=g, device="cuda") * 3).to(dtype)
+    got = silu_mul(x)
+    gate, up = x.split(1376, -1)
+    want = F.silu(gate) * up
+    ulp = 2.0 ** -10 if dtype == torch.float16 else 2.0 ** -7
+    assert torch.all((got.float() - want.float()).abs() <= 2 * ulp * want.float().abs() + 1e-6)
+
+
+def test_greedy_step_kernel():
+    """argmax with ties (first index), recording, and the state advance of
+    real rows; padding rows only take the token."""
+    announce("greedy step")
+    g = torch.Generator(device="cuda").manual_seed(2)
+    b, vocab = 6, 50000
+    logits = torch.randn(b, vocab, generator=g, device="cuda")
+    logits[2, 100] = logits[2, 40000] = 50.0  # a tie: first index wins
+    ids = torch.zeros(b, dtype=torch.int64, device="cuda")
+    pos = torch.tensor([15, 0, 31, 7, 200, 0], dtype=torch.int64, device="cuda")
+    ctx = (pos + 1).int()
+    slots = torch.zeros(b, dtype=torch.int64, device="cuda")
+    tables = torch.arange(b * 8, dtype=torch.int32, device="cuda").view(b, 8) + 1000
+    active = torch.tensor([1, 1, 1, 1, 1, 0], dtype=torch.int32, device="cuda")
+    ctx_start = ctx.clone()
+    tokens = torch.full((b, 4), -1, dtype=torch.int64, device="cuda")
+    greedy_step(logits, ids, pos, ctx, slots, tables, 16, active, ctx_start, tokens, 9999)
+    want = logits.argmax(-1)
+    assert want[2].item() == 100 and torch.equal(ids, want)
+    assert torch.equal(tokens[:5, 0], want[:5]) and tokens[5, 0].item() == -1
+    assert pos.tolist() == [16, 1, 32, 8, 201, 0] and ctx.tolist() == [17, 2, 33, 9, 202, 1]
+    t = tables.cpu()
+    want_slots = [int(t[r, p // 16]) * 16 + p % 16 for r, p in enumerate([16, 1, 32, 8])] + [9999, 0]
+    assert slots.tolist() == want_slots  # row 4: position 201 is past the 8-block table (128 tokens)
