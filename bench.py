@@ -30,6 +30,9 @@ verify       speculative verification's attention (16 sequences x 5 tokens)
 add_rms_norm the fused residual add + RMSNorm at three model shapes:
              algorithmic bytes (x and residual read, residual and output
              written, weight once) / mean kernel time, against 8 TB/s
+decode_step  a whole Llama-3-8B-shaped decode step (random weights, config 3's
+             64 sequences): eager, graph replay and on-device greedy chain,
+             bf16 and INT8 projections; bytes (weights + K/V) / step time
 int8_matmul  the INT8 weight-only matmul at Llama-3-8B decode projections
              (and Nimbus's own TinyLlama bench shape): algorithmic bytes
              (int8 weights, x, y, scales) / mean kernel time, against 8 TB/s,
@@ -464,6 +467,87 @@ def time_int8_matmul(steps, warmup):
     return res
 
 
+# ---------------------------------------------------------------- whole-model decode step
+
+def time_decode_step(steps, warmup, chain=16):
+    """One decode step of a Llama-3-8B-shaped model (32 layers, random bf16
+    weights) for the 64 sequences of BASELINE config 3 (contexts
+    log-uniform [128, 8192]), through DecodeGraphs: eager, one graph replay
+    per step, and greedy_chain (step graph + on-device token pick, no host
+    round trip); then the same with the decoder projections quantized to
+    INT8. Bytes per step: every weight once (int8 projections after
+    quantization) + every layer's visible K/V rows + the new K/V rows."""
+    import random
+
+    import torch
+
+    from nimbus_amd import workloads
+    from nimbus_amd.graphs import DecodeGraphs
+    from nimbus_amd.model.config import LLAMA3_8B as cfg
+    from nimbus_amd.model.llama import build_model
+    from nimbus_amd.model.runner import Sequence, prepare
+    from nimbus_amd.quant import quantize_model, weight_bytes
+
+    bs = 16
+    ctx = workloads.llama3_decode_lens(seed=0, batch=64)
+    max_len = 8192 + 2 * chain + 64
+    model = build_model(cfg, torch.bfloat16, "cuda", seed=0, max_position=max_len)
+    rng = random.Random(0)
+    need = sum(-(-(c + 2 * chain + 8) // bs) for c in ctx)
+    pool = rng.sample(range(need + 64), need + 64)
+    shape = (need + 65, bs, cfg.num_kv_heads, cfg.head_dim)  # the last block is the scratch block
+    g = torch.Generator(device="cuda").manual_seed(1)
+    caches = [(torch.randn(shape, generator=g, device="cuda").mul_(0.5).bfloat16(),
+               torch.randn(shape, generator=g, device="cuda").mul_(0.5).bfloat16()) for _ in range(cfg.num_layers)]
+    seqs = []
+    for i, c in enumerate(ctx):
+        s = Sequence(i, [rng.randrange(cfg.vocab_size) for _ in range(c)])
+        s.num_computed = c - 1
+        s.block_table = [pool.pop() for _ in range(-(-(c + 2 * chain + 8) // bs))]
+        seqs.append(s)
+    kv_bytes = sum(ctx) * cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
+
+    def measure(label):
+        wb = weight_bytes(model)
+        graphs = DecodeGraphs(model, caches, bs, max_len, 64, need + 64, cfg.num_kv_heads, "cuda", max_chain=chain)
+        graphs.capture()
+        batch = [(s, 1) for s in seqs]
+        for _ in range(warmup):
+            st = prepare(batch, bs, "cuda")
+            model.logits(model(st.input_ids, st.positions, caches, st.meta))
+        torch.cuda.synchronize()
+        n = max(3, steps // 10)
+        t0 = time.perf_counter()
+        for _ in range(n):
+            st = prepare(batch, bs, "cuda")
+            model.logits(model(st.input_ids, st.positions, caches, st.meta))
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) * 1e3 / n
+        for _ in range(warmup):
+            graphs.run(seqs)
+        replay_ms = statistics.mean(event_times_us(lambda i: graphs.run(seqs), n, torch.cuda.current_stream())) / 1e3
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        graphs.greedy_chain(seqs, chain)
+        torch.cuda.synchronize()
+        chain_ms = (time.perf_counter() - t0) * 1e3 / chain
+        nbytes = wb + kv_bytes + 64 * cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
+        del graphs
+        return {"weights": label, "weight_bytes": wb, "bytes_per_step": nbytes, "eager_ms": eager_ms,
+                "graph_replay_ms": replay_ms, "greedy_chain_ms_per_step": chain_ms,
+                "tokens_per_s": 64 / (chain_ms * 1e-3), "GBps": nbytes / (chain_ms * 1e-3) / 1e9,
+                "frac_hbm_peak": nbytes / (chain_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+    res = {"workload": "Llama-3-8B shape (random weights), 64 decode sequences of BASELINE config 3 "
+                       f"(sum ctx {sum(ctx)}), chains of {chain} greedy steps",
+           "runs": [measure("bf16")]}
+    quantize_model(model)
+    res["runs"].append(measure("int8 projections (bf16 embeddings and head)"))
+    del model, caches
+    torch.cuda.empty_cache()
+    return res
+
+
 # ---------------------------------------------------------------- --all
 
 def all_configs(steps, warmup):
@@ -578,6 +662,9 @@ def main(argv=None):
         log("int8_matmul")
         result["int8_matmul"] = time_int8_matmul(args.steps, args.warmup)
         log(f"int8_matmul: {result['int8_matmul']}")
+        log("decode_step (whole model)")
+        result["decode_step"] = time_decode_step(args.steps, args.warmup)
+        log(f"decode_step: {result['decode_step']}")
     if args.all:
         result["configs"] = {k: {a: b for a, b in v.items() if not isinstance(b, dict)}
                              for k, v in all_configs(args.steps, args.warmup).items()}
