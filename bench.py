@@ -433,8 +433,10 @@ def _graph_us(calls, steps, warmup):
 
 
 def time_int8_matmul(steps, warmup):
-    """int8_matmul at decode shapes: algorithmic bytes (the int8 weights, x,
-    y and the scales once) per kernel time, against 8 TB/s, and beside it
+    """The INT8 matmul at decode shapes on the tile-order weights Int8Linear
+    keeps (int8_matmul_packed; the row-major int8_matmul timed beside it):
+    algorithmic bytes (the int8 weights, x, y and the scales once) per
+    kernel time, against 8 TB/s, and beside it
     torch's dense matmul (hipBLASLt) on the same weights dequantized to the
     activation dtype, the comparison of Nimbus's own kernel bench
     (int8 vs fp16 cuBLAS). Calls run back to back in a hipGraph over
@@ -442,7 +444,8 @@ def time_int8_matmul(steps, warmup):
     256 MB Infinity Cache."""
     import torch
 
-    from nimbus_amd.kernels.int8_matmul import int8_matmul, int8_matmul_workspace_bytes
+    from nimbus_amd.kernels.int8_matmul import (int8_matmul, int8_matmul_packed, int8_matmul_packed_workspace_bytes,
+                                                int8_matmul_workspace_bytes, pack_int8_weight)
     from nimbus_amd.quant import dequantize_weight, quantize_weight
 
     res = []
@@ -454,15 +457,21 @@ def time_int8_matmul(steps, warmup):
                  for _ in range(n_pools)]
         x = torch.randn(m, k, generator=g, device="cuda").to(dtype)
         out = torch.empty(m, n, dtype=dtype, device="cuda")
-        ws = torch.empty(max(256, int8_matmul_workspace_bytes(m, n, k)), dtype=torch.uint8, device="cuda")
-        us = _graph_us([lambda q=q, s=s: int8_matmul(x, q, s, out=out, workspace=ws) for q, s in pools],
+        ws = torch.empty(max(256, int8_matmul_workspace_bytes(m, n, k), int8_matmul_packed_workspace_bytes(m, n, k)),
+                         dtype=torch.uint8, device="cuda")
+        row_us = _graph_us([lambda q=q, s=s: int8_matmul(x, q, s, out=out, workspace=ws) for q, s in pools],
+                           steps, warmup)
+        packed = [(pack_int8_weight(q), s) for q, s in pools]
+        us = _graph_us([lambda p=p, s=s: int8_matmul_packed(x, p, s, n, k, out=out, workspace=ws) for p, s in packed],
                        steps, warmup)
+        del packed
         nbytes = n * k + 2 * m * k + 2 * m * n + 2 * n
         dense = [dequantize_weight(q, s) for q, s in pools[:max(2, n_pools // 2)]]  # 2 bytes a weight
         dus = _graph_us([lambda d=d: torch.matmul(x, d.T, out=out) for d in dense], steps, warmup)
         res.append({"shape": name, "m": m, "n": n, "k": k, "dtype": dt, "us_per_call": us, "bytes": nbytes,
                     "GBps": nbytes / us / 1e3, "frac_hbm_peak": nbytes / us / 1e3 / HBM_PEAK_GBS,
-                    "dense_matmul_us": dus, "speedup_vs_dense": dus / us, "calls_per_replay": n_pools})
+                    "row_major_us_per_call": row_us, "dense_matmul_us": dus, "speedup_vs_dense": dus / us,
+                    "calls_per_replay": n_pools})
         del pools, dense
     return res
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 6
+#define NIMBUS_ATTN_ABI_VERSION 8
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -219,6 +219,40 @@ int64_t nimbus_int8_matmul_workspace_bytes(int64_t m, int32_t n, int32_t k);
 int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w_q, int64_t w_stride, const void* scale,
                        void* y, int64_t y_stride, int64_t m, int32_t n, int32_t k, void* workspace,
                        int64_t workspace_bytes, int32_t dtype, void* stream);
+
+/*
+ * The INT8 matmul on weights packed in MFMA tile order. Same y as
+ * nimbus_int8_matmul (the Triton kernel it replaces reads w_q [N, K] row by
+ * row; Int8Linear packs once, when a layer is quantized, so every call
+ * streams the weights in 1 KB contiguous pieces). Packed layout: block
+ * (nb, kc) of [ceil(n/16)][ceil(k/64)] is 1024 bytes; bytes 16 l .. 16 l + 15
+ * of a block hold row 16 nb + l % 16, columns 64 kc + 16 (l / 16) .. +16,
+ * zero padded past n and k. n a multiple of 4, k of 8; x, w_packed and y
+ * 16-byte aligned, scale 8-byte aligned; x_stride a multiple of 8,
+ * y_stride of 4. The workspace rule is nimbus_int8_matmul's, sized by
+ * nimbus_int8_matmul_packed_workspace_bytes.
+ */
+int64_t nimbus_int8_packed_weight_bytes(int32_t n, int32_t k);
+int nimbus_int8_pack_weight(const void* w_q, int64_t w_stride, int32_t n, int32_t k, void* out, void* stream);
+int64_t nimbus_int8_matmul_packed_workspace_bytes(int64_t m, int32_t n, int32_t k);
+int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const void* w_packed, const void* scale, void* y,
+                              int64_t y_stride, int64_t m, int32_t n, int32_t k, void* workspace,
+                              int64_t workspace_bytes, int32_t dtype, void* stream);
+
+/*
+ * nimbus_int8_matmul_packed with an explicit launch plan, for a caller that
+ * tunes per shape (as the reference's triton.autotune does per M bucket,
+ * N and K): bm tokens per workgroup tile (16, 32 or 64), ks k slices per
+ * workgroup (1, 2, 4 or 8, with ks * bm <= 128), splits of K (1..16). Any
+ * valid plan gives y to fp32 summation order; the workspace is
+ * nimbus_int8_matmul_packed_plan_workspace_bytes (-1 for an invalid plan).
+ */
+int64_t nimbus_int8_matmul_packed_plan_workspace_bytes(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
+                                                       int32_t splits);
+int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* w_packed, const void* scale, void* y,
+                                   int64_t y_stride, int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
+                                   int32_t splits, void* workspace, int64_t workspace_bytes, int32_t dtype,
+                                   void* stream);
 
 /*
  * Rotary position embedding, in place. Replaces Rotary.forward

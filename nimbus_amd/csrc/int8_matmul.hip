@@ -290,6 +290,292 @@ static int launch_gemm_dt(const GemmArgs& a, hipStream_t s) {
   }
 }
 
+// ---------------------------------------------------------------- packed weights
+//
+// nimbus_int8_matmul_packed takes the weights in MFMA tile order (built once
+// by nimbus_int8_pack_weight when a layer is quantized): block (nb, kc) of
+// [ceil(N/16)][ceil(K/64)] is 1024 bytes, lane l's 16 at offset 16 l holding
+// row 16 nb + l % 16, k = 64 kc + 16 (l / 16) .. +16 (zero padded), i.e.
+// exactly the A operand one 16-byte load per lane feeds. A wave's weight
+// loads are therefore 1 KB contiguous, and a wave streams one contiguous run
+// of 16 K bytes. The 8 waves of a workgroup are RB row blocks x KS k slices
+// (RB x KS = 8, BM x KS = 128): waves of one row block take interleaved
+// 64-k chunks and their sums are added in LDS at the end (fixed order), so
+// narrow matrices need no cross-workgroup split for small M.
+
+constexpr int kPackRing = 6;  // steps of loads in flight
+
+template <int BM, int KS>
+struct PackShape {
+  static constexpr int RB = kGemmWaves / KS;                 // row blocks per workgroup
+  static constexpr int XP = BM * KS * 8;                     // 16-byte x pieces per step
+  static constexpr int XC = (XP + kGemmThreads - 1) / kGemmThreads;  // pieces a thread stages per step
+};
+
+// Grid: (ceil(N / 16 / RB) row tiles, splits, M / BM token tiles).
+template <int DT, int BM, int KS>
+__global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmArgs a) {
+  constexpr int CB = BM / 16;
+  constexpr int RB = PackShape<BM, KS>::RB;
+  constexpr int XP = PackShape<BM, KS>::XP;
+  constexpr int XC = PackShape<BM, KS>::XC;
+  static_assert((KS - 1) * RB * CB * 1024 <= 2 * KS * BM * kXRow, "the k-slice sums fit the x buffers");
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][KS * BM * kXRow];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+  const int lane = tid % 64;
+  const int col = lane % 16;
+  const int grp = lane / 16;
+  const int ks = wave % KS;
+  const int rb = wave / KS;
+  const int nblocks = (a.N + 15) / 16;
+  const int kchunks = (a.K + 63) / 64;
+  const int nb = blockIdx.x * RB + rb;
+  const int c0 = blockIdx.y * (a.ksplit / 64);         // first 64-k chunk of this split
+  const int ce = min(kchunks, c0 + a.ksplit / 64);     // chunk end
+  const int m0 = blockIdx.z * BM;
+  const int steps = (ce - c0 + KS - 1) / KS;
+
+  const __amdgpu_buffer_rsrc_t wrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(a.w), 0, __builtin_amdgcn_readfirstlane(a.w_bytes), kBufferFlags);
+  const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(a.x), 0, __builtin_amdgcn_readfirstlane(a.x_bytes), kBufferFlags);
+  // Step s: this wave's chunk is c0 + KS s + ks of row block nb (blocks past
+  // the last read the last one and are never stored).
+  const uint32_t woff = static_cast<uint32_t>((min(nb, nblocks - 1) * kchunks + c0 + ks) * 1024 + 16 * lane);
+  auto load_w = [&](int s) {
+    const bool on = c0 + KS * s + ks < ce;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         wrsrc, on ? woff + KS * 1024 * s : kOutOfRange, 0, 0));
+  };
+  // x: piece q = tid + 512 i (< XP) of a step is chunk j = q / (8 BM) of the
+  // step, token (q % (8 BM)) / 8, elements 8 (q % 8) .. +8.
+  uint32_t xoff[XC];
+  int xk[XC], xs_off[XC];
+  bool x_on[XC], x_mine[XC];
+#pragma unroll
+  for (int i = 0; i < XC; ++i) {
+    const int q = tid + kGemmThreads * i;
+    const int j = q / (8 * BM);
+    const int tok = (q % (8 * BM)) / 8;
+    const int ch = q % 8;
+    x_mine[i] = q < XP;
+    x_on[i] = x_mine[i] && m0 + tok < a.M;
+    xk[i] = 64 * (c0 + j) + 8 * ch;
+    xoff[i] = x_on[i] ? static_cast<uint32_t>(2 * ((m0 + tok) * a.sx + xk[i])) : 0u;
+    xs_off[i] = (j * BM + tok) * kXRow + 16 * ch;
+  }
+  const int x_end = min(a.K, 64 * ce);
+  auto load_x = [&](int s, int i) {
+    const bool on = x_on[i] && xk[i] + 64 * KS * s < x_end;
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                         xrsrc, on ? xoff[i] + 2 * 64 * KS * s : kOutOfRange, 0, 0));
+  };
+  auto stage_x = [&](int buf, const u32x4* v) {
+#pragma unroll
+    for (int i = 0; i < XC; ++i) {
+      if (XP % kGemmThreads == 0 || x_mine[i]) *reinterpret_cast<u32x4*>(&xs[buf][xs_off[i]]) = v[i];
+    }
+  };
+
+  u32x4 wr[kPackRing], xr[kPackRing][XC];
+#pragma unroll
+  for (int r = 0; r < kPackRing; ++r) {
+    wr[r] = load_w(r);
+#pragma unroll
+    for (int i = 0; i < XC; ++i) xr[r][i] = load_x(r, i);
+  }
+  stage_x(0, xr[0]);
+  lds_barrier();
+
+  f32x4 acc[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int xb_off = (ks * BM + col) * kXRow + 32 * grp;
+
+  // One step: consume ring slot r (step s), optionally refill it with step
+  // s + kPackRing, stage x(s + 1), barrier.
+  auto step = [&](int s, int r, bool refill, u32x4& wslot, u32x4* xslot, const u32x4* xnext) {
+    const uint8_t* xb = &xs[s & 1][xb_off];
+    const u32x4 a0 = i8x8_to_operand<DT>(wslot[0], wslot[1]);
+    const u32x4 a1 = i8x8_to_operand<DT>(wslot[2], wslot[3]);
+    if (refill) {
+      wslot = load_w(s + kPackRing);
+#pragma unroll
+      for (int i = 0; i < XC; ++i) xslot[i] = load_x(s + kPackRing, i);
+      __builtin_amdgcn_sched_barrier(0);  // issue the refill now, not after this step's MFMAs
+    }
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const u32x4 b0 = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow);
+      const u32x4 b1 = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow + 16);
+      acc[cb] = mfma_16x16x32<DT>(a0, b0, acc[cb]);
+      acc[cb] = mfma_16x16x32<DT>(a1, b1, acc[cb]);
+    }
+    stage_x((s + 1) & 1, xnext);
+    lds_barrier();
+  };
+
+  // Whole rings with refills, then the remaining steps without (the ring's
+  // registers keep their places; no step past the range is computed).
+  int s0 = 0;
+  for (; s0 + kPackRing <= steps; s0 += kPackRing) {
+#pragma unroll
+    for (int r = 0; r < kPackRing; ++r) step(s0 + r, r, true, wr[r], xr[r], xr[(r + 1) % kPackRing]);
+  }
+#pragma unroll
+  for (int r = 0; r < kPackRing; ++r) {
+    if (s0 + r < steps) step(s0 + r, r, false, wr[r], xr[r], xr[(r + 1) % kPackRing]);
+  }
+
+  // Sum the KS k slices of each row block in slice order (LDS reuses the x
+  // buffers: every wave passed the last barrier).
+  if constexpr (KS > 1) {
+    f32x4* red = reinterpret_cast<f32x4*>(&xs[0][0]);  // [KS - 1][RB][CB][64 lanes]
+    if (ks > 0) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) red[(((ks - 1) * RB + rb) * CB + cb) * 64 + lane] = acc[cb];
+    }
+    lds_barrier();
+    if (ks > 0) return;
+#pragma unroll
+    for (int j = 1; j < KS; ++j) {
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) acc[cb] += red[(((j - 1) * RB + rb) * CB + cb) * 64 + lane];
+    }
+  }
+
+  const int n = 16 * nb + 4 * grp;
+  if (n >= a.N) return;
+  if (a.splits == 1) {
+    const u32x2 sw = *reinterpret_cast<const u32x2*>(a.scale + n);
+    const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
+                         Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int m = m0 + 16 * cb + col;
+      if (m < a.M) {
+        const f32x4 o = acc[cb];
+        const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(o[0] * sc[0]), Elem<DT>::from_f32(o[1] * sc[1])),
+                              pack2(Elem<DT>::from_f32(o[2] * sc[2]), Elem<DT>::from_f32(o[3] * sc[3]))};
+        *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const int m = m0 + 16 * cb + col;
+      if (m < a.M) {
+        float* p = a.part + (static_cast<int64_t>(blockIdx.y) * a.M + m) * a.N + n;
+        *reinterpret_cast<f32x4*>(p) = acc[cb];
+      }
+    }
+  }
+}
+
+// Packs int8 [N, K] (row stride ws bytes) into the tile order above: one
+// thread per 16-byte lane piece of a block.
+__global__ __launch_bounds__(256) void int8_pack_kernel(const int8_t* w, int64_t ws, int32_t n, int32_t k,
+                                                         int8_t* out) {
+  const int64_t kchunks = (k + 63) / 64;
+  const int64_t pieces = ((n + 15) / 16) * kchunks * 64;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= pieces) return;
+  const int lane = static_cast<int>(idx % 64);
+  const int64_t blk = idx / 64;
+  const int64_t kc = blk % kchunks;
+  const int64_t nb = blk / kchunks;
+  const int64_t row = 16 * nb + lane % 16;
+  const int64_t k0 = 64 * kc + 16 * (lane / 16);
+  uint8_t v[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) v[e] = (row < n && k0 + e < k) ? static_cast<uint8_t>(w[row * ws + k0 + e]) : 0;
+  u32x4 o;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    o[d] = static_cast<uint32_t>(v[4 * d]) | (static_cast<uint32_t>(v[4 * d + 1]) << 8) |
+           (static_cast<uint32_t>(v[4 * d + 2]) << 16) | (static_cast<uint32_t>(v[4 * d + 3]) << 24);
+  }
+  *reinterpret_cast<u32x4*>(out + idx * 16) = o;
+}
+
+static int64_t packed_bytes(int32_t n, int32_t k) {
+  return static_cast<int64_t>((n + 15) / 16) * ((k + 63) / 64) * 1024;
+}
+
+// k slices per workgroup: the fewest that still give every CU a workgroup
+// (longer per-workgroup streams), but enough row blocks that x, read once
+// per workgroup, stays within 2x the weight bytes (16 RB >= BM); then K
+// splits if the row tiles alone still leave CUs idle. A pure function of
+// the shape.
+struct PackPlan {
+  int bm, ks;
+  int32_t splits, ksplit;
+};
+
+static PackPlan packed_plan(int64_t m, int32_t n, int32_t k) {
+  PackPlan p;
+  p.bm = gemm_bm(m);
+  const int64_t nblocks = (n + 15) / 16;
+  const int64_t mtiles = (m + p.bm - 1) / p.bm;
+  const int max_ks = kGemmWaves * 16 / p.bm;  // 16 RB >= BM
+  p.ks = max_ks;
+  for (int ks = 1; ks <= max_ks; ks *= 2) {
+    const int rb = kGemmWaves / ks;
+    if ((nblocks + rb - 1) / rb * mtiles >= kFillWorkgroups) {
+      p.ks = ks;
+      break;
+    }
+  }
+  const int rb = kGemmWaves / p.ks;
+  const int64_t tiles = (nblocks + rb - 1) / rb * mtiles;
+  const int64_t step_k = 64 * p.ks;
+  int64_t s = 1;
+  if (tiles < kFillWorkgroups) s = (kFillWorkgroups + tiles - 1) / tiles;
+  if (s > kMaxSplits) s = kMaxSplits;
+  if (s > k / (4 * step_k)) s = k / (4 * step_k);  // at least four steps a split
+  if (s < 1) s = 1;
+  const int64_t kp = (k + 63) / 64 * 64;
+  int64_t ksp = (kp + s - 1) / s;
+  ksp = (ksp + step_k - 1) / step_k * step_k;
+  p.ksplit = static_cast<int32_t>(ksp);
+  p.splits = static_cast<int32_t>((kp + ksp - 1) / ksp);
+  return p;
+}
+
+template <int DT, int BM, int KS>
+static int launch_packed(const GemmArgs& a, hipStream_t s) {
+  constexpr int RB = PackShape<BM, KS>::RB;
+  const dim3 grid(((a.N + 15) / 16 + RB - 1) / RB, a.splits, (a.M + BM - 1) / BM);
+  hipLaunchKernelGGL((int8_matmul_packed_kernel<DT, BM, KS>), grid, dim3(kGemmThreads), 0, s, a);
+  if (a.splits > 1) {
+    const int64_t quads = static_cast<int64_t>(a.M) * (a.N / 4);
+    hipLaunchKernelGGL((int8_matmul_reduce_kernel<DT>), dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256),
+                       0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int DT, int BM>
+static int launch_packed_bm(const GemmArgs& a, int ks, hipStream_t s) {
+  switch (ks) {
+    case 1: return launch_packed<DT, BM, 1>(a, s);
+    case 2: return launch_packed<DT, BM, 2>(a, s);
+    case 4: if constexpr (BM <= 32) return launch_packed<DT, BM, 4>(a, s); else return NIMBUS_ERR_UNSUPPORTED;
+    default: if constexpr (BM <= 16) return launch_packed<DT, BM, 8>(a, s); else return NIMBUS_ERR_UNSUPPORTED;
+  }
+}
+
+template <int DT>
+static int launch_packed_dt(const GemmArgs& a, const PackPlan& p, hipStream_t s) {
+  switch (p.bm) {
+    case 16: return launch_packed_bm<DT, 16>(a, p.ks, s);
+    case 32: return launch_packed_bm<DT, 32>(a, p.ks, s);
+    default: return launch_packed_bm<DT, 64>(a, p.ks, s);
+  }
+}
+
 }  // namespace nimbus
 
 using namespace nimbus;
@@ -339,4 +625,114 @@ extern "C" int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w
   a.part = static_cast<float*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dtype == kFloat16 ? launch_gemm_dt<kFloat16>(a, s) : launch_gemm_dt<kBFloat16>(a, s);
+}
+
+extern "C" int64_t nimbus_int8_packed_weight_bytes(int32_t n, int32_t k) {
+  if (n <= 0 || k <= 0) return -1;
+  return packed_bytes(n, k);
+}
+
+extern "C" int nimbus_int8_pack_weight(const void* w_q, int64_t w_stride, int32_t n, int32_t k, void* out,
+                                       void* stream) {
+  if (n <= 0 || k <= 0 || w_stride < k) return NIMBUS_ERR_INVALID;
+  if (!w_q || !out) return NIMBUS_ERR_INVALID;
+  if (reinterpret_cast<uintptr_t>(out) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
+  const int64_t pieces = packed_bytes(n, k) / 16;
+  hipLaunchKernelGGL(int8_pack_kernel, dim3(static_cast<unsigned>((pieces + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const int8_t*>(w_q), w_stride, n, k,
+                     static_cast<int8_t*>(out));
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int64_t nimbus_int8_matmul_packed_workspace_bytes(int64_t m, int32_t n, int32_t k) {
+  if (m < 0 || n <= 0 || k <= 0) return -1;
+  const PackPlan p = packed_plan(m, n, k);
+  return p.splits > 1 ? static_cast<int64_t>(p.splits) * m * n * 4 : 0;
+}
+
+static int packed_impl(const void* x, int64_t x_stride, const void* w_packed, const void* scale, void* y,
+                       int64_t y_stride, int64_t m, int32_t n, int32_t k, const PackPlan* forced, void* workspace,
+                       int64_t workspace_bytes, int32_t dtype, void* stream) {
+  if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (n % 4 != 0 || k % 8 != 0) return NIMBUS_ERR_UNSUPPORTED;
+  if (m > (int64_t{1} << 21)) return NIMBUS_ERR_UNSUPPORTED;  // token tiles fit grid.z
+  if (m == 0) return NIMBUS_OK;
+  if (!x || !w_packed || !scale || !y) return NIMBUS_ERR_INVALID;
+  if (x_stride < k || y_stride < n) return NIMBUS_ERR_INVALID;
+  const int64_t x_bytes = ((m - 1) * x_stride + k) * 2;
+  const int64_t w_bytes = packed_bytes(n, k);
+  if (x_bytes >= (int64_t{1} << 31) || w_bytes >= (int64_t{1} << 31)) return NIMBUS_ERR_UNSUPPORTED;
+  if (x_stride % 8 != 0 || y_stride % 4 != 0) return NIMBUS_ERR_ALIGNMENT;
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed) | reinterpret_cast<uintptr_t>(y)) %
+              16 != 0 ||
+      reinterpret_cast<uintptr_t>(scale) % 8 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
+  GemmArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.sx = static_cast<int32_t>(x_stride);
+  a.w = static_cast<const int8_t*>(w_packed);
+  a.sw = 0;
+  a.x_bytes = static_cast<int32_t>(x_bytes);
+  a.w_bytes = static_cast<int32_t>(w_bytes);
+  a.scale = static_cast<const uint16_t*>(scale);
+  a.y = static_cast<uint16_t*>(y);
+  a.sy = y_stride;
+  a.M = static_cast<int32_t>(m);
+  a.N = n;
+  a.K = k;
+  const PackPlan plan = forced ? *forced : packed_plan(m, n, k);
+  a.splits = plan.splits;
+  a.ksplit = plan.ksplit;
+  const int64_t need = a.splits > 1 ? static_cast<int64_t>(a.splits) * m * n * 4 : 0;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return NIMBUS_ERR_WORKSPACE;
+  if (need > 0 && reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
+  a.part = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == kFloat16 ? launch_packed_dt<kFloat16>(a, plan, s) : launch_packed_dt<kBFloat16>(a, plan, s);
+}
+
+extern "C" int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const void* w_packed, const void* scale,
+                                         void* y, int64_t y_stride, int64_t m, int32_t n, int32_t k,
+                                         void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream) {
+  return packed_impl(x, x_stride, w_packed, scale, y, y_stride, m, n, k, nullptr, workspace, workspace_bytes, dtype,
+                     stream);
+}
+
+// An explicit plan: token tile bm (16, 32, 64), k slices ks (1, 2, 4, 8;
+// ks * bm <= 128) and k splits (1..16, fewer when K is short). Workspace:
+// splits * m * n * 4 bytes when the plan splits.
+static bool make_plan(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks, int32_t splits, PackPlan* p) {
+  (void)m;
+  (void)n;
+  if (bm != 16 && bm != 32 && bm != 64) return false;
+  if (ks != 1 && ks != 2 && ks != 4 && ks != 8) return false;
+  if (ks * bm > 128 || splits < 1 || splits > kMaxSplits) return false;
+  const int64_t step_k = 64 * ks;
+  const int64_t kp = (k + 63) / 64 * 64;
+  int64_t ksp = (kp + splits - 1) / splits;
+  ksp = (ksp + step_k - 1) / step_k * step_k;
+  p->bm = bm;
+  p->ks = ks;
+  p->ksplit = static_cast<int32_t>(ksp);
+  p->splits = static_cast<int32_t>((kp + ksp - 1) / ksp);
+  return true;
+}
+
+extern "C" int64_t nimbus_int8_matmul_packed_plan_workspace_bytes(int64_t m, int32_t n, int32_t k, int32_t bm,
+                                                                  int32_t ks, int32_t splits) {
+  PackPlan p;
+  if (m < 0 || n <= 0 || k <= 0 || !make_plan(m, n, k, bm, ks, splits, &p)) return -1;
+  return p.splits > 1 ? static_cast<int64_t>(p.splits) * m * n * 4 : 0;
+}
+
+extern "C" int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* w_packed,
+                                              const void* scale, void* y, int64_t y_stride, int64_t m, int32_t n,
+                                              int32_t k, int32_t bm, int32_t ks, int32_t splits, void* workspace,
+                                              int64_t workspace_bytes, int32_t dtype, void* stream) {
+  PackPlan p;
+  if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
+  if (!make_plan(m, n, k, bm, ks, splits, &p)) return NIMBUS_ERR_UNSUPPORTED;
+  return packed_impl(x, x_stride, w_packed, scale, y, y_stride, m, n, k, &p, workspace, workspace_bytes, dtype,
+                     stream);
 }

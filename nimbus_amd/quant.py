@@ -13,7 +13,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from nimbus_amd.kernels.int8_matmul import int8_matmul
+from nimbus_amd.kernels.int8_matmul import int8_matmul_packed, pack_int8_weight, unpack_int8_weight
 
 
 def quantize_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -33,7 +33,11 @@ def dequantize_weight(q: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
 class Int8Linear(nn.Module):
     """nimbus/quant/int8.py:32-47 with the HIP kernel. The reference keeps a
     PyTorch path behind use_triton=False; this module is the GPU path only,
-    so use_hip=False is refused rather than served on the CPU."""
+    so use_hip=False is refused rather than served on the CPU.
+
+    The quantized weight is kept in the kernel's tile order
+    (`weight_packed`, packed once here); `weight_q` gives it back as the
+    reference's int8 [out, in] for inspection."""
 
     def __init__(self, linear: nn.Linear, use_hip: bool = True):
         super().__init__()
@@ -42,12 +46,16 @@ class Int8Linear(nn.Module):
         if linear.bias is not None:
             raise ValueError("the decoder projections have no bias")
         q, s = quantize_weight(linear.weight.data)
-        self.register_buffer("weight_q", q)
+        self.register_buffer("weight_packed", pack_int8_weight(q))
         self.register_buffer("scale", s)
         self.in_features, self.out_features = linear.in_features, linear.out_features
 
+    @property
+    def weight_q(self) -> torch.Tensor:
+        return unpack_int8_weight(self.weight_packed, self.out_features, self.in_features)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return int8_matmul(x, self.weight_q, self.scale)
+        return int8_matmul_packed(x, self.weight_packed, self.scale, self.out_features, self.in_features)
 
 
 QUANTIZED = ("qkv_proj", "o_proj", "gate_up_proj", "down_proj")

@@ -5,7 +5,9 @@ rtol 1e-2 of fp32(x @ w_q^T) * scale rounded to the element type, on its
 matrix of M in {1, 7, 64, 300} and TinyLlama's projection shapes, in fp16.
 Added: bf16 and Llama-3-8B shapes, an exact check on small integers (pins
 the int8 -> fp16/bf16 widening bit for bit), shapes whose N and K leave
-partial tiles and steps, strided activations, and repeatability.
+partial tiles and steps, strided activations, and repeatability. Every
+product check runs on both weight layouts: row-major w_q (int8_matmul) and
+the tile order Int8Linear packs (int8_matmul_packed).
 """
 
 from __future__ import annotations
@@ -13,12 +15,19 @@ from __future__ import annotations
 import pytest
 import torch
 
-from nimbus_amd.kernels.int8_matmul import int8_matmul, int8_matmul_workspace_bytes
+from nimbus_amd.kernels.int8_matmul import (int8_matmul, int8_matmul_packed, int8_matmul_workspace_bytes,
+                                            pack_int8_weight, unpack_int8_weight)
 from nimbus_amd.quant import Int8Linear, quantize_weight
 from oracle import closed_form, reference
 from tests.gpu_helpers import announce
 
 pytestmark = pytest.mark.gpu
+
+
+def _mm(x, q, s, packed):
+    if packed:
+        return int8_matmul_packed(x, pack_int8_weight(q), s, q.shape[0], q.shape[1])
+    return int8_matmul(x, q, s)
 
 
 def _case(m, n, k, dtype, seed):
@@ -29,40 +38,45 @@ def _case(m, n, k, dtype, seed):
     return x, q, s
 
 
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("m", [1, 7, 64, 300])
 @pytest.mark.parametrize("n,k", [(3072, 2048), (2048, 5632), (11264, 2048)])
-def test_reference_matrix_fp16(m, n, k):
-    announce(f"int8_matmul fp16 m={m} n={n} k={k} ws={int8_matmul_workspace_bytes(m, n, k)}")
+def test_reference_matrix_fp16(m, n, k, packed):
+    announce(f"int8_matmul fp16 m={m} n={n} k={k} packed={packed} ws={int8_matmul_workspace_bytes(m, n, k)}")
     x, q, s = _case(m, n, k, torch.float16, m * 7 + n + k)
-    got = int8_matmul(x, q, s)
+    got = _mm(x, q, s, packed)
     want = reference.int8_matmul(x.cpu(), q.cpu(), s.cpu())
     torch.cuda.synchronize()
     torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("m", [1, 16, 64, 130])
 @pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336), (28672, 4096)])
-def test_llama3_shapes_bf16(m, n, k):
-    announce(f"int8_matmul bf16 m={m} n={n} k={k}")
+def test_llama3_shapes_bf16(m, n, k, packed):
+    announce(f"int8_matmul bf16 m={m} n={n} k={k} packed={packed}")
     x, q, s = _case(m, n, k, torch.bfloat16, m + n + k)
-    got = int8_matmul(x, q, s)
+    got = _mm(x, q, s, packed)
     want = reference.int8_matmul(x.cpu(), q.cpu(), s.cpu())
     torch.cuda.synchronize()
     torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("m,n,k", [(5, 260, 96), (33, 4100, 1040), (64, 128, 8192), (1, 4, 16)])
-def test_small_integers_are_exact(dtype, m, n, k):
+@pytest.mark.parametrize("m,n,k", [(5, 260, 96), (33, 4100, 1040), (64, 128, 8192), (1, 4, 16), (130, 36, 4104)])
+def test_small_integers_are_exact(dtype, m, n, k, packed):
     """Integer x and w_q with power-of-two scales: every product and partial
     sum is exact in fp32, so the kernel must equal the float64 product
     rounded once, whatever the tiling or K split."""
-    announce(f"int8_matmul exact {dtype} m={m} n={n} k={k}")
+    announce(f"int8_matmul exact {dtype} m={m} n={n} k={k} packed={packed}")
+    if not packed and k % 16:
+        pytest.skip("the row-major kernel takes K in multiples of 16")
     g = torch.Generator(device="cuda").manual_seed(m * n + k)
     x = torch.randint(-3, 4, (m, k), generator=g, device="cuda").to(dtype)
     q = torch.randint(-127, 128, (n, k), generator=g, device="cuda").to(torch.int8)
     s = (2.0 ** -torch.randint(6, 10, (n,), generator=g, device="cuda").float()).to(dtype)
-    got = int8_matmul(x, q, s)
+    got = _mm(x, q, s, packed)
     want = torch.from_numpy(closed_form.int8_matmul(x.cpu(), q.cpu(), s.cpu())).to(dtype)
     torch.cuda.synchronize()
     assert torch.equal(got.cpu(), want)
@@ -114,3 +128,50 @@ def test_zero_rows_and_explicit_workspace():
     assert torch.equal(out, int8_matmul(x, q, s))
     with pytest.raises(ValueError):
         int8_matmul(x, q, s, workspace=ws[:need - 16])
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (260, 1040), (3072, 2048), (5, 24)])
+def test_pack_unpack_roundtrip_and_layout(n, k):
+    """The tile order of nimbus_int8_matmul_packed: block (nb, kc), lane l's
+    16 bytes = row 16 nb + l % 16, columns 64 kc + 16 (l / 16) .. +16, zero
+    padded; unpacking gives w_q back."""
+    announce(f"pack n={n} k={k}")
+    g = torch.Generator(device="cuda").manual_seed(n + k)
+    q = torch.randint(-127, 128, (n, k), generator=g, device="cuda").to(torch.int8)
+    p = pack_int8_weight(q)
+    assert p.shape == (-(-n // 16), -(-k // 64), 1024)
+    assert torch.equal(unpack_int8_weight(p, n, k), q)
+    qc, pc = q.cpu(), p.cpu()
+    nb, kc, lane, e = p.shape[0] - 1, p.shape[1] - 1, 37, 5
+    row, colk = 16 * nb + lane % 16, 64 * kc + 16 * (lane // 16) + e
+    want = int(qc[row, colk]) if row < n and colk < k else 0
+    assert int(pc[nb, kc, 16 * lane + e]) == want
+
+
+@pytest.mark.parametrize("m,n,k", [(33, 4100, 1040), (64, 4096, 4096), (7, 6144, 4096), (1, 260, 8192)])
+def test_every_launch_plan_is_exact(m, n, k):
+    """Each plan the tuner may pick (token tile, k slices, K splits) gives
+    the float64 product rounded once on integer inputs, so tuning can only
+    change speed."""
+    from nimbus_amd import _lib
+    from nimbus_amd.kernels import int8_matmul as mod
+
+    announce(f"int8 plans m={m} n={n} k={k}")
+    g = torch.Generator(device="cuda").manual_seed(m + n)
+    x = torch.randint(-3, 4, (m, k), generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randint(-127, 128, (n, k), generator=g, device="cuda").to(torch.int8)
+    s = (2.0 ** -torch.randint(6, 10, (n,), generator=g, device="cuda").float()).to(torch.bfloat16)
+    want = torch.from_numpy(closed_form.int8_matmul(x.cpu(), q.cpu(), s.cpu())).to(torch.bfloat16)
+    p = pack_int8_weight(q)
+    lib = _lib.load()
+    plans = mod._candidate_plans(m, n, k)
+    assert plans
+    for plan in plans:
+        need = lib.nimbus_int8_matmul_packed_plan_workspace_bytes(m, n, k, *plan)
+        ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        rc = lib.nimbus_int8_matmul_packed_plan(x.data_ptr(), k, p.data_ptr(), s.data_ptr(), y.data_ptr(), n, m, n, k,
+                                                *plan, ws.data_ptr(), ws.numel(), 1, None)
+        assert rc == 0, plan
+        torch.cuda.synchronize()
+        assert torch.equal(y.cpu(), want), plan
