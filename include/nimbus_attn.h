@@ -262,7 +262,8 @@ int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* 
  * positions[t] row of the fp32 cos / sin tables (row stride table_stride),
  * with every multiply and the add rounded to dtype as the reference's ops
  * are. Tokens whose position is outside [0, max_position) are left as is.
- * head_dim a multiple of 16; x 16-byte aligned, x_stride a multiple of 8.
+ * head_dim a multiple of 16; x 16-byte aligned, x_stride a multiple of 8;
+ * the tables 16-byte aligned with table_stride a multiple of 4.
  */
 int nimbus_rope(void* x, int64_t x_stride, int64_t num_tokens, int32_t num_heads, int32_t head_dim,
                 const int64_t* positions, const float* cos_table, const float* sin_table, int64_t table_stride,

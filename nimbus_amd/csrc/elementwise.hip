@@ -60,19 +60,28 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   uint16_t* row = a.x + t * a.sx + static_cast<int64_t>(h) * a.d;
   const u32x4 lo = *reinterpret_cast<const u32x4*>(row + i0);
   const u32x4 hi = *reinterpret_cast<const u32x4*>(row + half + i0);
+  // The table rows' 8 entries at i0 and at i0 + D/2, as 16-byte loads.
   const float* cr = a.cos + p * a.st;
   const float* sr = a.sin + p * a.st;
+  float c_lo[8], s_lo[8], c_hi[8], s_hi[8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    *reinterpret_cast<f32x4*>(&c_lo[4 * h]) = *reinterpret_cast<const f32x4*>(cr + i0 + 4 * h);
+    *reinterpret_cast<f32x4*>(&s_lo[4 * h]) = *reinterpret_cast<const f32x4*>(sr + i0 + 4 * h);
+    *reinterpret_cast<f32x4*>(&c_hi[4 * h]) = *reinterpret_cast<const f32x4*>(cr + half + i0 + 4 * h);
+    *reinterpret_cast<f32x4*>(&s_hi[4 * h]) = *reinterpret_cast<const f32x4*>(sr + half + i0 + 4 * h);
+  }
   u32x4 olo, ohi;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     uint16_t out_lo[2], out_hi[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
-      const int i = i0 + 2 * e + b;
+      const int j = 2 * e + b;
       const float xl = Elem<DT>::to_f32(static_cast<uint16_t>(lo[e] >> (16 * b)));
       const float xh = Elem<DT>::to_f32(static_cast<uint16_t>(hi[e] >> (16 * b)));
-      const float cl = rnd<DT>(cr[i]), sl = rnd<DT>(sr[i]);
-      const float ch = rnd<DT>(cr[i + half]), sh = rnd<DT>(sr[i + half]);
+      const float cl = rnd<DT>(c_lo[j]), sl = rnd<DT>(s_lo[j]);
+      const float ch = rnd<DT>(c_hi[j]), sh = rnd<DT>(s_hi[j]);
       // x * cos + rotate_half(x) * sin, rotate_half(x) = cat(-x_hi, x_lo)
       out_lo[b] = Elem<DT>::from_f32(rnd<DT>(xl * cl) + rnd<DT>(-xh * sl));
       out_hi[b] = Elem<DT>::from_f32(rnd<DT>(xh * ch) + rnd<DT>(xl * sh));
@@ -142,43 +151,58 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-// One 256-thread workgroup per row.
-__global__ __launch_bounds__(256) void greedy_step_kernel(GreedyArgs a) {
+constexpr int kGreedyThreads = 1024;
+
+__device__ __forceinline__ void consider(float v, int i, float& bv, int& bi) {
+  if (better(v, i, bv, bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+// One 1024-thread workgroup per row. With 16-byte aligned rows, each thread
+// reads float4 pieces 1024 apart, four loads in flight before any compare.
+__global__ __launch_bounds__(kGreedyThreads) void greedy_step_kernel(GreedyArgs a) {
   const int row = blockIdx.x;
+  const int tid = threadIdx.x;
   const float* lr = a.logits + static_cast<int64_t>(row) * a.sl;
   float bv = -INFINITY;
   int bi = a.vocab;
-  for (int i = threadIdx.x; i < a.vocab; i += 256) {
-    const float v = lr[i];
-    if (better(v, i, bv, bi)) {
-      bv = v;
-      bi = i;
+  const bool vec = (a.sl % 4 == 0) && (reinterpret_cast<uintptr_t>(a.logits) % 16 == 0);
+  const int nvec = vec ? a.vocab / 4 : 0;
+  const f32x4* lv = reinterpret_cast<const f32x4*>(lr);
+  int i = tid;
+  for (; i + 3 * kGreedyThreads < nvec; i += 4 * kGreedyThreads) {
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = lv[i + u * kGreedyThreads];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) consider(v[u][e], 4 * (i + u * kGreedyThreads) + e, bv, bi);
     }
   }
+  for (; i < nvec; i += kGreedyThreads) {
+    const f32x4 v = lv[i];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) consider(v[e], 4 * i + e, bv, bi);
+  }
+  for (int j = 4 * nvec + tid; j < a.vocab; j += kGreedyThreads) consider(lr[j], j, bv, bi);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
     const int oi = __shfl_xor(bi, off, 64);
-    if (better(ov, oi, bv, bi)) {
-      bv = ov;
-      bi = oi;
-    }
+    consider(ov, oi, bv, bi);
   }
-  __shared__ float sv[4];
-  __shared__ int si[4];
-  const int wave = threadIdx.x / 64;
-  if (threadIdx.x % 64 == 0) {
-    sv[wave] = bv;
-    si[wave] = bi;
+  __shared__ float sv[kGreedyThreads / 64];
+  __shared__ int si[kGreedyThreads / 64];
+  if (tid % 64 == 0) {
+    sv[tid / 64] = bv;
+    si[tid / 64] = bi;
   }
   __syncthreads();
-  if (threadIdx.x != 0) return;
-  for (int w = 1; w < 4; ++w) {
-    if (better(sv[w], si[w], bv, bi)) {
-      bv = sv[w];
-      bi = si[w];
-    }
-  }
+  if (tid != 0) return;
+  for (int w = 1; w < kGreedyThreads / 64; ++w) consider(sv[w], si[w], bv, bi);
   const int64_t tok = bi < a.vocab ? bi : 0;  // a row of NaNs picks token 0
   a.input_ids[row] = tok;
   if (!a.active[row]) return;
@@ -226,7 +250,7 @@ extern "C" int nimbus_greedy_step(const float* logits, int64_t logits_stride, in
   a.tokens = tokens;
   a.max_steps = max_steps;
   a.scratch_slot = scratch_slot;
-  hipLaunchKernelGGL(greedy_step_kernel, dim3(rows), dim3(256), 0, static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(greedy_step_kernel, dim3(rows), dim3(kGreedyThreads), 0, static_cast<hipStream_t>(stream), a);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -240,6 +264,9 @@ extern "C" int nimbus_rope(void* x, int64_t x_stride, int64_t num_tokens, int32_
   if (!x || !positions || !cos_table || !sin_table) return NIMBUS_ERR_INVALID;
   if (x_stride < static_cast<int64_t>(num_heads) * head_dim || table_stride < head_dim) return NIMBUS_ERR_INVALID;
   if (x_stride % 8 != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
+  if (table_stride % 4 != 0 ||
+      (reinterpret_cast<uintptr_t>(cos_table) | reinterpret_cast<uintptr_t>(sin_table)) % 16 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
   RopeArgs a;
   a.x = static_cast<uint16_t*>(x);
   a.sx = x_stride;

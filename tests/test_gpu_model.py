@@ -229,14 +229,18 @@ def test_silu_mul_kernel(dtype):
     assert torch.all((got.float() - want.float()).abs() <= 2 * ulp * want.float().abs() + 1e-6)
 
 
-def test_greedy_step_kernel():
+@pytest.mark.parametrize("vocab,stride", [(50000, 50000), (50001, 50004), (32003, 32003), (128256, 128256)])
+def test_greedy_step_kernel(vocab, stride):
     """argmax with ties (first index), recording, and the state advance of
-    real rows; padding rows only take the token."""
-    announce("greedy step")
+    real rows; padding rows only take the token. Rows with 16-byte aligned
+    starts take the vector path (with a scalar tail when vocab % 4 != 0),
+    others the scalar path."""
+    announce(f"greedy step vocab={vocab} stride={stride}")
     g = torch.Generator(device="cuda").manual_seed(2)
-    b, vocab = 6, 50000
-    logits = torch.randn(b, vocab, generator=g, device="cuda")
-    logits[2, 100] = logits[2, 40000] = 50.0  # a tie: first index wins
+    b = 6
+    logits = torch.randn(b, stride, generator=g, device="cuda")[:, :vocab]
+    logits[2, 100] = logits[2, 40000 % vocab] = 50.0  # a tie: first index wins
+    logits[3, vocab - 1] = 60.0  # the maximum in the last (tail) element
     ids = torch.zeros(b, dtype=torch.int64, device="cuda")
     pos = torch.tensor([15, 0, 31, 7, 200, 0], dtype=torch.int64, device="cuda")
     ctx = (pos + 1).int()
@@ -247,7 +251,7 @@ def test_greedy_step_kernel():
     tokens = torch.full((b, 4), -1, dtype=torch.int64, device="cuda")
     greedy_step(logits, ids, pos, ctx, slots, tables, 16, active, ctx_start, tokens, 9999)
     want = logits.argmax(-1)
-    assert want[2].item() == 100 and torch.equal(ids, want)
+    assert want[2].item() == 100 and want[3].item() == vocab - 1 and torch.equal(ids, want)
     assert torch.equal(tokens[:5, 0], want[:5]) and tokens[5, 0].item() == -1
     assert pos.tolist() == [16, 1, 32, 8, 201, 0] and ctx.tolist() == [17, 2, 33, 9, 202, 1]
     t = tables.cpu()
