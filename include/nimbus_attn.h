@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 8
+#define NIMBUS_ATTN_ABI_VERSION 9
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -147,6 +147,30 @@ int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, 
                          int32_t num_programs, void* out, int64_t out_stride_t, int64_t out_stride_h,
                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
                          int32_t dtype, void* stream);
+
+/*
+ * nimbus_paged_prefill with heavy tiles' key ranges cut into pieces, for
+ * batches whose tiles alone would leave the chip idle while the heaviest
+ * tile walks its keys. pieces: [num_pieces][5] int32 = (sequence, first
+ * query offset of a NIMBUS_PREFILL_TILE tile, first key block, end key block
+ * (64-key blocks; INT32_MAX = to the causal end), workspace slot or -1 for a
+ * whole tile written straight to out). A split tile's pieces write fp32
+ * (O, m, l) rows to consecutive slots; merges: [num_merges][4] int32 =
+ * (sequence, first query offset, first slot, pieces) combines them into out
+ * (o = sum O_i 2^(m_i - M) / sum l_i 2^(m_i - M)). Slots at or past
+ * num_slots are never written. Workspace:
+ * nimbus_paged_prefill_pieces_workspace_bytes(num_slots, num_heads, head_dim).
+ */
+int64_t nimbus_paged_prefill_pieces_workspace_bytes(int32_t num_slots, int32_t num_heads, int32_t head_dim);
+int nimbus_paged_prefill_pieces(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                                const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                                int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                                int64_t bt_stride, int32_t bt_width, const int32_t* query_start,
+                                const int32_t* context_lens, const int32_t* pieces, int32_t num_pieces,
+                                const int32_t* merges, int32_t num_merges, int32_t num_slots, void* workspace,
+                                int64_t workspace_bytes, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                float scale, int32_t dtype, void* stream);
 
 /*
  * Bytes of workspace nimbus_paged_verify needs (as for the decode workspace,

@@ -25,7 +25,7 @@ NIMBUS_ERR_INVALID = -1
 NIMBUS_ERR_UNSUPPORTED = -2
 NIMBUS_ERR_ALIGNMENT = -3
 NIMBUS_ERR_WORKSPACE = -4
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # Entry points and their C signatures, in the order include/nimbus_attn.h declares them.
 _c_int, _c_i32, _c_i64, _c_p, _c_f = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
@@ -43,6 +43,11 @@ SIGNATURES = {
     "nimbus_paged_prefill": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
                                       _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_i32,
                                       _c_i32, _c_i32, _c_f, _c_i32, _c_p]),
+    "nimbus_paged_prefill_pieces_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32]),
+    "nimbus_paged_prefill_pieces": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p,
+                                             _c_i64, _c_i32, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_i32, _c_p,
+                                             _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f,
+                                             _c_i32, _c_p]),
     "nimbus_paged_verify_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i64]),
     "nimbus_paged_verify": None,
     "nimbus_add_rms_norm": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i32,

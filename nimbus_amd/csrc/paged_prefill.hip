@@ -34,6 +34,15 @@
 //                                              with ds_read_b64_tr_b16, P^T is
 //                                              the QK output layout as is
 // Causal and context masks are applied only on blocks that need them.
+//
+// Key-range pieces (nimbus_paged_prefill_pieces). When a batch has too few
+// tiles to fill the chip, the heaviest tile's serial walk over its key
+// blocks sets the time. The host then cuts heavy tiles' key ranges into
+// pieces [kb0, kb1) of about equal length; a piece writes its rows'
+// unnormalised fp32 O with the running max m and row sum l to a workspace
+// slot, and paged_prefill_merge_kernel combines a tile's pieces with
+// o = sum_i O_i 2^(m_i - M) / sum_i l_i 2^(m_i - M), M = max m_i (the rule
+// decode's split pieces use).
 #include <type_traits>
 
 #include "common.h"
@@ -59,9 +68,13 @@ struct PrefillArgs {
   const int32_t* ctx;
   const int32_t* prog_seq;
   const int32_t* prog_m;
+  const int32_t* pieces;  // [units][5]: seq, m0, kb0, kb1, slot (-1: whole); null: the plain tile table
+  float* part;            // workspace: per slot [64 positions][H] rows of D floats of O, then (m, l) pairs
+  int64_t part_ml;        // float offset of the (m, l) pairs: slots * 64 * H * D
+  int32_t slots;          // workspace slots (a piece's slot at or past it is not written)
   uint16_t* out;
   int64_t o_st, o_sh;
-  int32_t G, gsplit, kvg;
+  int32_t H, G, gsplit, kvg;
   float scale_log2;
 };
 
@@ -132,15 +145,29 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   const int sub = r_unit % Shape::kSub;
   const int kvh = kvg_id / a.gsplit;
   const int gsub = kvg_id % a.gsplit;
-  const int seq = a.prog_seq[entry];
-  const int m0 = a.prog_m[entry] + sub * POS;
+  int seq, m_entry, kb0 = 0, kb1 = INT32_MAX, slot = -1;
+  if (a.pieces) {
+    const int32_t* pe = a.pieces + 5 * entry;
+    seq = pe[0];
+    m_entry = pe[1];
+    kb0 = pe[2];
+    kb1 = pe[3];
+    slot = pe[4];
+  } else {
+    seq = a.prog_seq[entry];
+    m_entry = a.prog_m[entry];
+  }
+  const int m0 = m_entry + sub * POS;
   const int qs = a.qstart[seq];
   const int q_len = a.qstart[seq + 1] - qs;
   if (m0 >= q_len) return;  // the whole workgroup: this sub-tile has no queries
   const int ctx = min(a.ctx[seq], a.bt_width * 16);
   const int base_pos = ctx - q_len;  // absolute position of query 0
   const int kv_end = max(0, min(ctx, base_pos + m0 + POS));
-  const int n_kb = (kv_end + kBlockN - 1) / kBlockN;
+  // This unit's key blocks [kbeg, kend): all of them, or its piece's share.
+  const int n_kb_all = (kv_end + kBlockN - 1) / kBlockN;
+  const int kbeg = min(kb0, n_kb_all);
+  const int kend = min(kb1, n_kb_all);
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64) & (Shape::kWaves - 1);  // scalar, range known
@@ -369,18 +396,18 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // one barrier, which also waits for the K copies. The page ids of a block
   // are read one iteration before its loads are issued.
   Scores sa, sb;
-  BlockPages pg_v = load_pages(1);  // pages of V(kb + 1)
-  BlockPages pg_k = load_pages(2);  // pages of K(kb + 2)
-  if (n_kb > 0) {
-    const BlockPages pg0 = load_pages(0);
-    issue_v(pg0, 0);
-    dma_k(pg0, 0, IntC<0>{});
+  BlockPages pg_v = load_pages(kbeg + 1);  // pages of V(kb + 1)
+  BlockPages pg_k = load_pages(kbeg + 2);  // pages of K(kb + 2)
+  if (kend > kbeg) {
+    const BlockPages pg0 = load_pages(kbeg);
+    issue_v(pg0, kbeg);
+    dma_k(pg0, kbeg, IntC<0>{});
     __syncthreads();
-    dma_k(pg_v, 1, IntC<1>{});  // past the context: zeros
+    dma_k(pg_v, kbeg + 1, IntC<1>{});  // past the context: zeros; past the piece: unused
     qk(IntC<0>{}, IntC<0>{}, sa);
     qk(IntC<0>{}, IntC<1>{}, sa);
     store_v(IntC<0>{});
-    mask_and_max(sa, 0);
+    mask_and_max(sa, kbeg);
     __syncthreads();
   }
   auto iteration = [&](int kb, auto slot, auto has_k2, auto has_next, Scores& s_cur, Scores& s_nxt) {
@@ -413,21 +440,39 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     pg_v = pg_k;
     if constexpr (K2) pg_k = pg_n;
   };
-  int kb = 0;
-  for (; kb + 3 < n_kb; kb += 2) {
+  int kb = kbeg;
+  for (; kb + 3 < kend; kb += 2) {
     iteration(kb, IntC<0>{}, BoolC<true>{}, BoolC<true>{}, sa, sb);
     iteration(kb + 1, IntC<1>{}, BoolC<true>{}, BoolC<true>{}, sb, sa);
   }
-  // kb is even here; 0 to 3 iterations remain.
-  if (kb + 2 < n_kb) {
+  // kb - kbeg is even here; 0 to 3 iterations remain.
+  if (kb + 2 < kend) {
     iteration(kb, IntC<0>{}, BoolC<true>{}, BoolC<true>{}, sa, sb);
     iteration(kb + 1, IntC<1>{}, BoolC<false>{}, BoolC<true>{}, sb, sa);
     iteration(kb + 2, IntC<0>{}, BoolC<false>{}, BoolC<false>{}, sa, sb);
-  } else if (kb + 1 < n_kb) {
+  } else if (kb + 1 < kend) {
     iteration(kb, IntC<0>{}, BoolC<false>{}, BoolC<true>{}, sa, sb);
     iteration(kb + 1, IntC<1>{}, BoolC<false>{}, BoolC<false>{}, sb, sa);
-  } else if (kb < n_kb) {
+  } else if (kb < kend) {
     iteration(kb, IntC<0>{}, BoolC<false>{}, BoolC<false>{}, sa, sb);
+  }
+
+  if (slot >= 0) {
+    if (slot >= a.slots) return;
+    // A piece: unnormalised O^T, the running max and the row sum, per row
+    // (rows past q_len are skipped; a row that saw no key here keeps
+    // m = -inf, l = 0, O = 0 and weighs nothing in the merge).
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      if (!row_ok[nb]) continue;
+      const int pos = m0 - m_entry + (32 * wave + 16 * nb + col) / GS;
+      const int64_t row = (static_cast<int64_t>(slot) * kPrefillTile + pos) * a.H + head[nb];
+      float* po = a.part + row * D;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) *reinterpret_cast<f32x4*>(po + 16 * nd + 4 * grp) = acc[nd][nb];
+      if (grp == 0) *reinterpret_cast<float2*>(a.part + a.part_ml + row * 2) = make_float2(m_run[nb], lsum[nb][0]);
+    }
+    return;
   }
 
 #pragma unroll
@@ -446,6 +491,55 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   }
 }
 
+// Combines the pieces of split tiles: one thread per (tile, position, head,
+// 8 elements of D). merges: [num_merges][4] = seq, m0, first slot, pieces.
+template <int DT, int D>
+__global__ __launch_bounds__(256) void paged_prefill_merge_kernel(PrefillArgs a, const int32_t* merges,
+                                                                  int32_t num_merges) {
+  constexpr int SEG = D / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t per_tile = static_cast<int64_t>(kPrefillTile) * a.H * SEG;
+  if (idx >= per_tile * num_merges) return;
+  const int e = static_cast<int>(idx / per_tile);
+  const int rem = static_cast<int>(idx % per_tile);
+  const int pos = rem / (a.H * SEG);
+  const int head = (rem / SEG) % a.H;
+  const int d0 = 8 * (rem % SEG);
+  const int32_t* me = merges + 4 * e;
+  const int seq = me[0], m0 = me[1], slot0 = me[2], n = me[3];
+  if (slot0 < 0 || n <= 0 || slot0 + n > a.slots) return;
+  const int qs = a.qstart[seq];
+  if (m0 + pos >= a.qstart[seq + 1] - qs) return;
+  float M = -INFINITY;
+  for (int i = 0; i < n; ++i) {
+    const int64_t row = (static_cast<int64_t>(slot0 + i) * kPrefillTile + pos) * a.H + head;
+    M = fmaxf(M, a.part[a.part_ml + row * 2]);
+  }
+  float L = 0.f, O[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) O[k] = 0.f;
+  for (int i = 0; i < n; ++i) {
+    const int64_t row = (static_cast<int64_t>(slot0 + i) * kPrefillTile + pos) * a.H + head;
+    const float2 ml = *reinterpret_cast<const float2*>(a.part + a.part_ml + row * 2);
+    const float w = ml.x == -INFINITY ? 0.f : fast_exp2(ml.x - M);
+    const f32x4 o0 = *reinterpret_cast<const f32x4*>(a.part + row * D + d0);
+    const f32x4 o1 = *reinterpret_cast<const f32x4*>(a.part + row * D + d0 + 4);
+    L += ml.y * w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      O[k] += o0[k] * w;
+      O[k + 4] += o1[k] * w;
+    }
+  }
+  const float inv = 1.f / L;
+  uint16_t* orow = a.out + static_cast<int64_t>(qs + m0 + pos) * a.o_st + static_cast<int64_t>(head) * a.o_sh + d0;
+  const u32x4 w4 = u32x4{pack2(Elem<DT>::from_f32(O[0] * inv), Elem<DT>::from_f32(O[1] * inv)),
+                         pack2(Elem<DT>::from_f32(O[2] * inv), Elem<DT>::from_f32(O[3] * inv)),
+                         pack2(Elem<DT>::from_f32(O[4] * inv), Elem<DT>::from_f32(O[5] * inv)),
+                         pack2(Elem<DT>::from_f32(O[6] * inv), Elem<DT>::from_f32(O[7] * inv))};
+  *reinterpret_cast<u32x4*>(orow) = w4;
+}
+
 // One kernel per register budget (the occupancy attribute takes a constant).
 template <int DT, int D, int GS>
 __global__ __launch_bounds__(PrefillShape<GS>::kThreads) __attribute__((amdgpu_waves_per_eu(2))) void
@@ -457,6 +551,15 @@ template <int DT, int D, int GS>
 __global__ __launch_bounds__(PrefillShape<GS>::kThreads) __attribute__((amdgpu_waves_per_eu(1))) void
 paged_prefill_kernel_1w(PrefillArgs a) {
   prefill_unit<DT, D, GS>(a);
+}
+
+template <int DT, int D>
+static int launch_merge(const PrefillArgs& a, const int32_t* merges, int32_t num_merges, hipStream_t stream) {
+  if (num_merges <= 0) return static_cast<int>(hipGetLastError());
+  const int64_t threads = static_cast<int64_t>(num_merges) * kPrefillTile * a.H * (D / 8);
+  hipLaunchKernelGGL((paged_prefill_merge_kernel<DT, D>), dim3(static_cast<unsigned>((threads + 255) / 256)),
+                     dim3(256), 0, stream, a, merges, num_merges);
+  return static_cast<int>(hipGetLastError());
 }
 
 template <int DT, int D, int GS>
@@ -492,16 +595,16 @@ static int dispatch_gs(const PrefillArgs& a, int gs, int num_programs, hipStream
 
 using namespace nimbus;
 
-extern "C" int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
-                                    const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
-                                    int64_t cache_stride_token, int64_t cache_stride_head,
-                                    const int32_t* block_tables, int64_t bt_stride, int32_t bt_width,
-                                    const int32_t* query_start, const int32_t* context_lens,
-                                    const int32_t* prog_seq, const int32_t* prog_m, int32_t num_programs,
-                                    void* out, int64_t out_stride_t, int64_t out_stride_h, int32_t num_heads,
-                                    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
-                                    int32_t dtype, void* stream) {
-  if (num_programs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
+static int prefill_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                        const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                        int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                        int64_t bt_stride, int32_t bt_width, const int32_t* query_start, const int32_t* context_lens,
+                        const int32_t* prog_seq, const int32_t* prog_m, const int32_t* pieces, int32_t num_units,
+                        const int32_t* merges, int32_t num_merges, int32_t num_slots, void* workspace,
+                        int64_t workspace_bytes, void* out, int64_t out_stride_t, int64_t out_stride_h,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                        int32_t dtype, void* stream) {
+  if (num_units < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return NIMBUS_ERR_INVALID;
   if (block_size != 16) return NIMBUS_ERR_UNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return NIMBUS_ERR_UNSUPPORTED;
@@ -509,9 +612,9 @@ extern "C" int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q
   const int G = num_heads / num_kv_heads;
   // Heads per unit: the largest of 8, 4, 2, 1 that divides G.
   const int gs = G % 8 == 0 ? 8 : (G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1));
-  if (num_programs == 0) return NIMBUS_OK;
-  if (!q || !k_cache || !v_cache || !block_tables || !query_start || !context_lens || !prog_seq || !prog_m || !out)
-    return NIMBUS_ERR_INVALID;
+  if (num_units == 0) return NIMBUS_OK;
+  if (!q || !k_cache || !v_cache || !block_tables || !query_start || !context_lens || !out) return NIMBUS_ERR_INVALID;
+  if (!pieces && (!prog_seq || !prog_m)) return NIMBUS_ERR_INVALID;
   if (num_blocks <= 0 || num_blocks > INT32_MAX || bt_width <= 0) return NIMBUS_ERR_INVALID;
   // Pages are read through buffer resources with 32-bit offsets: 16 token
   // rows of a page must span less than 2 GiB.
@@ -522,6 +625,12 @@ extern "C" int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k_cache) |
        reinterpret_cast<uintptr_t>(v_cache) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
     return NIMBUS_ERR_ALIGNMENT;
+  if (pieces) {
+    if (num_slots < 0 || num_merges < 0 || (num_merges > 0 && !merges)) return NIMBUS_ERR_INVALID;
+    const int64_t need = static_cast<int64_t>(num_slots) * kPrefillTile * num_heads * (head_dim + 2) * 4;
+    if (num_slots > 0 && (workspace == nullptr || workspace_bytes < need)) return NIMBUS_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
+  }
 
   PrefillArgs a;
   a.q = static_cast<const uint16_t*>(q);
@@ -540,19 +649,73 @@ extern "C" int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q
   a.ctx = context_lens;
   a.prog_seq = prog_seq;
   a.prog_m = prog_m;
+  a.pieces = pieces;
+  a.part = static_cast<float*>(workspace);
+  a.part_ml = static_cast<int64_t>(num_slots) * kPrefillTile * num_heads * head_dim;
+  a.slots = pieces ? num_slots : 0;
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_t;
   a.o_sh = out_stride_h;
+  a.H = num_heads;
   a.G = G;
   a.gsplit = G / gs;
   a.kvg = num_kv_heads * a.gsplit;
   a.scale_log2 = scale * 1.4426950408889634f;
 
   hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc;
   if (dtype == kFloat16) {
-    return head_dim == 64 ? dispatch_gs<kFloat16, 64>(a, gs, num_programs, s)
-                          : dispatch_gs<kFloat16, 128>(a, gs, num_programs, s);
+    rc = head_dim == 64 ? dispatch_gs<kFloat16, 64>(a, gs, num_units, s)
+                        : dispatch_gs<kFloat16, 128>(a, gs, num_units, s);
+  } else {
+    rc = head_dim == 64 ? dispatch_gs<kBFloat16, 64>(a, gs, num_units, s)
+                        : dispatch_gs<kBFloat16, 128>(a, gs, num_units, s);
   }
-  return head_dim == 64 ? dispatch_gs<kBFloat16, 64>(a, gs, num_programs, s)
-                        : dispatch_gs<kBFloat16, 128>(a, gs, num_programs, s);
+  if (rc != 0 || !pieces || num_merges == 0) return rc;
+  if (dtype == kFloat16) {
+    return head_dim == 64 ? launch_merge<kFloat16, 64>(a, merges, num_merges, s)
+                          : launch_merge<kFloat16, 128>(a, merges, num_merges, s);
+  }
+  return head_dim == 64 ? launch_merge<kBFloat16, 64>(a, merges, num_merges, s)
+                        : launch_merge<kBFloat16, 128>(a, merges, num_merges, s);
+}
+
+extern "C" int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                                    const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                                    int64_t cache_stride_token, int64_t cache_stride_head,
+                                    const int32_t* block_tables, int64_t bt_stride, int32_t bt_width,
+                                    const int32_t* query_start, const int32_t* context_lens,
+                                    const int32_t* prog_seq, const int32_t* prog_m, int32_t num_programs,
+                                    void* out, int64_t out_stride_t, int64_t out_stride_h, int32_t num_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                                    int32_t dtype, void* stream) {
+  return prefill_impl(q, q_stride_t, q_stride_h, k_cache, v_cache, num_blocks, cache_stride_block,
+                      cache_stride_token, cache_stride_head, block_tables, bt_stride, bt_width, query_start,
+                      context_lens, prog_seq, prog_m, nullptr, num_programs, nullptr, 0, 0, nullptr, 0, out,
+                      out_stride_t, out_stride_h, num_heads, num_kv_heads, head_dim, block_size, scale, dtype, stream);
+}
+
+extern "C" int64_t nimbus_paged_prefill_pieces_workspace_bytes(int32_t num_slots, int32_t num_heads,
+                                                               int32_t head_dim) {
+  if (num_slots < 0 || num_heads <= 0 || head_dim <= 0) return -1;
+  return static_cast<int64_t>(num_slots) * kPrefillTile * num_heads * (head_dim + 2) * 4;
+}
+
+extern "C" int nimbus_paged_prefill_pieces(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                                           const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                                           int64_t cache_stride_token, int64_t cache_stride_head,
+                                           const int32_t* block_tables, int64_t bt_stride, int32_t bt_width,
+                                           const int32_t* query_start, const int32_t* context_lens,
+                                           const int32_t* pieces, int32_t num_pieces, const int32_t* merges,
+                                           int32_t num_merges, int32_t num_slots, void* workspace,
+                                           int64_t workspace_bytes, void* out, int64_t out_stride_t,
+                                           int64_t out_stride_h, int32_t num_heads, int32_t num_kv_heads,
+                                           int32_t head_dim, int32_t block_size, float scale, int32_t dtype,
+                                           void* stream) {
+  if (!pieces) return NIMBUS_ERR_INVALID;
+  return prefill_impl(q, q_stride_t, q_stride_h, k_cache, v_cache, num_blocks, cache_stride_block,
+                      cache_stride_token, cache_stride_head, block_tables, bt_stride, bt_width, query_start,
+                      context_lens, nullptr, nullptr, pieces, num_pieces, merges, num_merges, num_slots, workspace,
+                      workspace_bytes, out, out_stride_t, out_stride_h, num_heads, num_kv_heads, head_dim,
+                      block_size, scale, dtype, stream);
 }

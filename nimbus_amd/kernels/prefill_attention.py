@@ -16,11 +16,14 @@ spend a 64-row tile on a handful of queries.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import numpy as np
 import torch
 
 from nimbus_amd import _lib
-from nimbus_amd.kernels.paged_attention import MAX_VERIFY_QUERIES, PAGE, _check_cache, paged_verify_attention
+from nimbus_amd.kernels.paged_attention import (MAX_VERIFY_QUERIES, PAGE, _cached_workspace, _check_cache,
+                                                paged_verify_attention)
 
 BLOCK_M = 64  # query positions per tile-table entry (NIMBUS_PREFILL_TILE)
 # Tiles whose workgroups all fit the chip at once: a GQA tile is typically 16
@@ -89,6 +92,78 @@ def build_programs(query_start_host: list[int], device,
     return t[0], t[1]
 
 
+KEY_BLOCK = 64  # keys per block of the prefill kernel's walk
+RESIDENT_WORKGROUPS = 512  # prefill workgroups a gfx950 part holds at once (256 CUs x 2)
+
+
+@dataclass
+class PrefillPieces:
+    """A tile table whose heavy tiles' key ranges are cut into pieces
+    (nimbus_paged_prefill_pieces): pieces [n, 5] and merges [m, 4] int32 on
+    the device, and the workspace slots the split pieces use."""
+
+    pieces: torch.Tensor
+    merges: torch.Tensor
+    num_slots: int
+
+
+def _units_per_tile(num_heads: int, num_kv_heads: int) -> int:
+    g = num_heads // num_kv_heads
+    gs = 8 if g % 8 == 0 else 4 if g % 4 == 0 else 2 if g % 2 == 0 else 1
+    pos = min(128 // gs, BLOCK_M)
+    return (BLOCK_M // pos) * num_kv_heads * (g // gs)
+
+
+def plan_pieces(query_start_host: list[int], context_lens_host: list[int], num_heads: int, num_kv_heads: int,
+                device, resident: int = RESIDENT_WORKGROUPS) -> PrefillPieces | None:
+    """Key-range pieces for a batch with fewer tiles than the chip holds at
+    once (a short chunk over a long cached prefix, say), so that idle CUs
+    take part of the heavy tiles' key walks; None otherwise, or when
+    splitting would not shorten the walk. (With the chip full, two tiles per
+    CU and the cost order pairing heavy with light already balance the work,
+    and pieces only add partial writes and a merge: measured slower.)
+
+    A tile's cost is the key blocks its last query sees. With H tiles held
+    on the chip at once, pieces aim at S = max(4, ceil(total blocks / H))
+    blocks: a tile of more than 1.25 S blocks is cut into ceil(blocks / S)
+    near-equal ranges. Pieces go heaviest first."""
+    qs = np.asarray(query_start_host, dtype=np.int64)
+    if qs.size < 2:
+        return None
+    lens = np.diff(qs)
+    tiles = (lens + BLOCK_M - 1) // BLOCK_M
+    seqs = np.repeat(np.arange(lens.size, dtype=np.int64), tiles)
+    if seqs.size == 0:
+        return None
+    first = np.repeat(np.cumsum(tiles) - tiles, tiles)
+    starts = (np.arange(seqs.size) - first) * BLOCK_M
+    ctx = np.asarray(context_lens_host, dtype=np.int64)
+    keys = np.maximum(np.minimum(ctx[seqs], ctx[seqs] - lens[seqs] + starts + BLOCK_M), 0)
+    blocks = (keys + KEY_BLOCK - 1) // KEY_BLOCK
+    hold = max(1, resident // _units_per_tile(num_heads, num_kv_heads))
+    if seqs.size >= hold:
+        return None  # the tiles fill the chip: two per CU, heavy paired with light, keep it busy already
+    s = max(4, -(-int(blocks.sum()) // hold))
+    if blocks.max() <= 1.25 * s:
+        return None
+    rows, merges, slot = [], [], 0
+    for sq, m0, nb in zip(seqs.tolist(), starts.tolist(), blocks.tolist()):
+        k = -(-nb // s) if nb > 1.25 * s else 1
+        if k == 1:
+            rows.append((nb, sq, m0, 0, 2**31 - 1, -1))
+            continue
+        edges = [round(i * nb / k) for i in range(k + 1)]
+        merges.append((sq, m0, slot, k))
+        for i in range(k):
+            rows.append((edges[i + 1] - edges[i], sq, m0, edges[i], edges[i + 1], slot + i))
+        slot += k
+    rows.sort(key=lambda r: -r[0])
+    table = np.asarray([r[1:] for r in rows], dtype=np.int32)
+    t = torch.from_numpy(table).to(device, non_blocking=True)
+    mt = torch.from_numpy(np.asarray(merges, dtype=np.int32).reshape(-1, 4)).to(device, non_blocking=True)
+    return PrefillPieces(t, mt, slot)
+
+
 def paged_prefill_attention(
     q: torch.Tensor,  # [Tp, H, D]
     k_cache: torch.Tensor,
@@ -108,11 +183,12 @@ def paged_prefill_attention(
 
     The cache must already hold the new tokens' K/V (write_kv runs first, as
     in nimbus/model/attention.py:78). `programs` is build_programs' tile table
-    (built here when None). Not in the reference signature: `out` receives
+    (built here when None), or a PrefillPieces plan (plan_pieces) that cuts
+    heavy tiles' key ranges. Not in the reference signature: `out` receives
     the result in place; `kernel` is "auto" (the verify form when
     verify_queries() takes the batch, else the tile kernel), "tile" or
-    "verify"; `workspace` is the verify form's (paged_verify_attention), by
-    default the per-stream cached one.
+    "verify"; `workspace` is the verify form's or the pieces' (by default
+    the per-stream cached one).
 
     The verify form bounds context lengths by the block-table width (16
     tokens a column), not by context_lens_host: Nimbus's verify graphs pass
@@ -149,9 +225,6 @@ def paged_prefill_attention(
                                       block_tables.shape[1] * PAGE, scale, out=out, workspace=workspace)
     if programs is None:
         programs = build_programs(query_start_host, q.device, context_lens_host)
-    prog_seq, prog_m = programs
-    if prog_seq.numel() == 0:
-        return out
     if q.stride(-1) != 1:
         q = q.contiguous()
     if block_tables.stride(1) != 1:
@@ -159,11 +232,27 @@ def paged_prefill_attention(
     query_start = query_start.contiguous()
     context_lens = context_lens.contiguous()
     lib = _lib.load()
-    rc = lib.nimbus_paged_prefill(
-        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
-        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(), block_tables.stride(0),
-        block_tables.shape[1], query_start.data_ptr(), context_lens.data_ptr(), prog_seq.data_ptr(),
-        prog_m.data_ptr(), prog_seq.numel(), out.data_ptr(), out.stride(0), out.stride(1), h, kv, d,
-        k_cache.shape[1], float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    common = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+              k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(),
+              block_tables.stride(0), block_tables.shape[1], query_start.data_ptr(), context_lens.data_ptr())
+    tail = (out.data_ptr(), out.stride(0), out.stride(1), h, kv, d, k_cache.shape[1], float(scale),
+            _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    if isinstance(programs, PrefillPieces):
+        need = lib.nimbus_paged_prefill_pieces_workspace_bytes(programs.num_slots, h, d)
+        if workspace is not None:
+            if workspace.numel() * workspace.element_size() < need or not workspace.is_cuda:
+                raise ValueError(f"workspace smaller than the {need} bytes this call needs")
+            ws = workspace
+        else:
+            ws = _cached_workspace(need, q.device)
+        rc = lib.nimbus_paged_prefill_pieces(
+            *common, programs.pieces.data_ptr(), programs.pieces.shape[0], programs.merges.data_ptr(),
+            programs.merges.shape[0], programs.num_slots, ws.data_ptr(), ws.numel() * ws.element_size(), *tail)
+        _lib.check(rc, "nimbus_paged_prefill_pieces")
+        return out
+    prog_seq, prog_m = programs
+    if prog_seq.numel() == 0:
+        return out
+    rc = lib.nimbus_paged_prefill(*common, prog_seq.data_ptr(), prog_m.data_ptr(), prog_seq.numel(), *tail)
     _lib.check(rc, "nimbus_paged_prefill")
     return out

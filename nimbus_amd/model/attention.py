@@ -37,7 +37,8 @@ class AttnMetadata:
     # Host copies, so nothing on the host waits for the GPU
     prefill_query_start_host: list[int]
     prefill_context_lens_host: list[int]
-    # Tile table, built once per step and reused by every layer
+    # Tile table, built once per step and reused by every layer (here it may
+    # also be a prefill_attention.PrefillPieces plan)
     prefill_programs: tuple[torch.Tensor, torch.Tensor] | None = None
     # Fixed decode launch grid of the reference's graph capture (accepted, unused:
     # the grid here is pinned by max_decode_context)
@@ -100,8 +101,12 @@ class AttentionBackend:
                 nq = prefill_attention.verify_queries(meta.prefill_query_start_host, q.shape[1], k_cache.shape[2])
                 meta.prefill_kernel = "verify" if nq else "tile"
             if meta.prefill_programs is None and meta.prefill_kernel == "tile":
-                meta.prefill_programs = self._build_programs(meta.prefill_query_start_host, q.device,
-                                                             meta.prefill_context_lens_host)
+                # Heavy tiles' key ranges cut into pieces when the tiles alone
+                # would not fill the chip, else the cost-ordered tile table.
+                meta.prefill_programs = prefill_attention.plan_pieces(
+                    meta.prefill_query_start_host, meta.prefill_context_lens_host, q.shape[1], k_cache.shape[2],
+                    q.device) or self._build_programs(meta.prefill_query_start_host, q.device,
+                                                      meta.prefill_context_lens_host)
             self._prefill(
                 q[:p], k_cache, v_cache, meta.prefill_query_start, meta.prefill_context_lens,
                 meta.prefill_block_tables, scale, meta.prefill_query_start_host,

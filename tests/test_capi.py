@@ -24,6 +24,7 @@ def test_header_declares_the_four_launch_paths():
     names = declared_functions()
     for want in ("nimbus_write_kv", "nimbus_paged_decode", "nimbus_paged_decode_workspace_bytes",
                  "nimbus_paged_prefill", "nimbus_paged_verify", "nimbus_paged_verify_workspace_bytes",
+                 "nimbus_paged_prefill_pieces", "nimbus_paged_prefill_pieces_workspace_bytes",
                  "nimbus_add_rms_norm", "nimbus_int8_matmul", "nimbus_int8_matmul_workspace_bytes",
                  "nimbus_attn_abi_version",
                  "nimbus_attn_error_string"):
@@ -190,3 +191,15 @@ def test_int8_workspace_is_splits_times_fp32_output():
     # rings of 512) -> 7 splits
     assert ws(16, 4096, 14336) == 7 * 16 * 4096 * 4
     assert ws(1, 3072, 2048) == 4 * 1 * 3072 * 4  # 24 tiles want 11 splits; 2048 / 512 allows 4
+
+
+def test_prefill_pieces_checks():
+    lib = _lib.load()
+    assert lib.nimbus_paged_prefill_pieces_workspace_bytes(3, 32, 128) == 3 * 64 * 32 * 130 * 4
+    assert lib.nimbus_paged_prefill_pieces_workspace_bytes(-1, 32, 128) == -1
+    base = [DUMMY, 32 * 128, 128, DUMMY, DUMMY, 100, 16 * 8 * 128, 8 * 128, 128, DUMMY, 4, 4, DUMMY, DUMMY]
+    tail = [DUMMY, 32 * 128, 128, 32, 8, 128, 16, 0.1, 1, None]
+    f = lib.nimbus_paged_prefill_pieces
+    assert f(*base, None, 3, None, 0, 0, None, 0, *tail) == _lib.NIMBUS_ERR_INVALID  # no piece table
+    assert f(*base, DUMMY, 3, DUMMY, 1, 2, None, 0, *tail) == _lib.NIMBUS_ERR_WORKSPACE  # slots need a workspace
+    assert f(*base, DUMMY, 0, None, 0, 0, None, 0, *tail) == 0  # no pieces: nothing to launch

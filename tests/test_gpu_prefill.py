@@ -12,7 +12,8 @@ import pytest
 import torch
 
 from nimbus_amd import workloads
-from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
+from nimbus_amd.kernels.prefill_attention import (PrefillPieces, build_programs, paged_prefill_attention,
+                                                  plan_pieces)
 from oracle import closed_form
 from tests import golden_io
 from tests.gpu_helpers import announce, oracle_prefill
@@ -95,3 +96,41 @@ def test_prefill_configs_full(config):
     got = paged_prefill_attention(*args)
     q, k, v, _, _, bt, scale, qs, ctx = args
     assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what=config)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("heads,kv,d,seqs,resident", [
+    (32, 8, 128, [(64, 8192), (130, 4000), (40, 300)], 512),                # short chunks on long prefixes
+    # a larger chip share per tile (resident) forces cuts on small batches
+    (32, 4, 64, [(130, 1000), (64, 64), (3, 700), (200, 201)], 2048),         # mixed batch
+    (8, 8, 64, [(70, 2000), (1, 9)], 2048),                                  # MHA, a single-token sequence
+    (12, 4, 128, [(100, 3000), (40, 1000)], 2048),                            # G = 3, partial tiles
+])
+def test_key_range_pieces_match_oracle(dtype, heads, kv, d, seqs, resident):
+    """Heavy tiles' key ranges cut into pieces (fp32 partials merged by the
+    log-sum-exp rule) give the oracle's output, and the uncut tile kernel's
+    within the bar."""
+    announce(f"prefill pieces H={heads} KV={kv} D={d} {dtype} seqs={seqs} resident={resident}")
+    q, k, v, qst, ctxt, bt, scale, qs, ctx = _case(heads, kv, d, seqs, dtype, seed=8)
+    plan = plan_pieces(qs, ctx, heads, kv, "cuda", resident=resident)
+    assert plan is not None and plan.num_slots > 0
+    got = paged_prefill_attention(q, k, v, qst, ctxt, bt, scale, qs, ctx, plan)
+    whole = paged_prefill_attention(q, k, v, qst, ctxt, bt, scale, qs, ctx, kernel="tile")
+    torch.cuda.synchronize()
+    assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="pieces vs oracle")
+    assert_within(got.cpu(), whole.cpu().double(), what="pieces vs whole tiles")
+
+
+def test_pieces_with_an_empty_sub_tile_range():
+    """A 64-query tile at context 660 (Llama-3 heads: two 32-position
+    sub-tiles): the second sub-tile sees 11 key blocks, the first only 10, so
+    the piece [10, end) holds nothing for the first sub-tile, whose rows must
+    write m = -inf, l = 0 and weigh nothing in the merge."""
+    announce("prefill pieces: empty sub-tile range")
+    q, k, v, qst, ctxt, bt, scale, qs, ctx = _case(32, 8, 128, [(64, 660)], torch.bfloat16, seed=9)
+    end = 2**31 - 1
+    pieces = torch.tensor([[0, 0, 10, end, 2], [0, 0, 4, 10, 1], [0, 0, 0, 4, 0]], dtype=torch.int32, device="cuda")
+    merges = torch.tensor([[0, 0, 0, 3]], dtype=torch.int32, device="cuda")
+    got = paged_prefill_attention(q, k, v, qst, ctxt, bt, scale, qs, ctx, PrefillPieces(pieces, merges, 3))
+    torch.cuda.synchronize()
+    assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="vs oracle")

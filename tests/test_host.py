@@ -192,3 +192,41 @@ def test_int8_matmul_wrapper_checks():
         int8_matmul(x.float(), q, s.float())
     with pytest.raises(ValueError):
         Int8Linear(torch.nn.Linear(64, 32, bias=False), use_hip=False)
+
+
+def test_plan_pieces_covers_every_block_once():
+    """Short chunks over long prefixes (6 tiles, Llama-3 heads): heavy tiles
+    are cut into near-equal ranges that tile their key blocks exactly, slots
+    are consecutive per tile, light tiles stay whole."""
+    from nimbus_amd.kernels.prefill_attention import KEY_BLOCK, plan_pieces
+
+    lens, prefix = [130, 64, 40], [4000, 8000, 300]  # few tiles over long prefixes: the chip is underfilled
+    qs = [0]
+    for n in lens:
+        qs.append(qs[-1] + n)
+    ctx = [p + n for p, n in zip(prefix, lens)]
+    plan = plan_pieces(qs, ctx, 32, 8, "cpu")
+    assert plan is not None
+    pieces, merges = plan.pieces.numpy(), plan.merges.numpy()
+    for seq, m0 in {(int(r[0]), int(r[1])) for r in pieces}:
+        rows = sorted((int(r[2]), int(r[3]), int(r[4])) for r in pieces if r[0] == seq and r[1] == m0)
+        blocks = -(-min(ctx[seq], ctx[seq] - lens[seq] + m0 + 64) // KEY_BLOCK)
+        if len(rows) == 1:
+            assert rows[0][2] == -1 and rows[0][0] == 0
+            continue
+        assert rows[0][0] == 0 and rows[-1][1] == blocks
+        assert all(a[1] == b[0] for a, b in zip(rows, rows[1:]))
+        slots = [r[2] for r in rows]
+        assert slots == list(range(slots[0], slots[0] + len(rows)))
+        assert [seq, m0, slots[0], len(rows)] in merges.tolist()
+    assert plan.num_slots == sum(int(m[3]) for m in merges) > 0
+
+
+def test_plan_pieces_declines_when_tiles_fill_the_chip():
+    from nimbus_amd.kernels.prefill_attention import plan_pieces
+
+    qs = list(range(0, 64 * 2048 + 1, 2048))  # 64 sequences x 32 tiles: far more than the chip holds at once
+    assert plan_pieces(qs, [4096] * 64, 32, 8, "cpu") is None
+    qs4 = [0, 512, 1024, 1536, 2048]  # config 4: 32 tiles fill the chip, two per CU
+    assert plan_pieces(qs4, [1512, 529, 1152, 1536], 32, 8, "cpu") is None
+    assert plan_pieces([0, 64], [64], 32, 8, "cpu") is None  # one short tile: nothing to cut
