@@ -18,9 +18,15 @@
 // number of bytes (+-1 page) whatever the mix of context lengths; a slice
 // may end inside one sequence and continue into the next.
 //
-// Each wave is its own workgroup (64 threads): no barriers, no atomics, no
-// state kept between calls. It first turns context_lens into the page
-// prefix sum in LDS, then walks its slice one page at a time. Decode is
+// The waves of the kv-head groups that read the same slice form one
+// workgroup (up to 8 waves) and meet at a barrier every kSyncPages pages.
+// Left to themselves the waves of different kv heads drift apart, and waves
+// reading the same pages at different times slow each other down (measured:
+// each kv head alone streams at one rate, but together some heads ended
+// 25% later than others); kept in step, the heads of a page are read
+// together and finish together. No atomics and no state are kept between
+// calls. Wave 0 first turns context_lens into the page prefix sum in LDS;
+// then every wave walks its kv group's slice one page at a time. Decode is
 // bound by HBM latency as much as bandwidth, so each wave keeps kRing pages
 // of K/V in flight in a ring of register buffers (page x + kRing is issued
 // as soon as page x has been consumed), and finds each page's id kRing + 2
@@ -56,6 +62,8 @@ constexpr int kPage = 16;             // tokens per page (the only block size)
 constexpr int kMinPagesPerWave = 8;   // slices shorter than this only add merge work
 constexpr int kMaxDecodeBatch = 4096; // LDS holds the batch's page prefix sum
 constexpr int kWavesPerCU = 8;        // two waves of the page kernel per SIMD
+constexpr int kMaxWgWaves = 8;        // waves (kv-head groups) per workgroup
+constexpr int kSyncPages = 4;         // pages between the workgroup's barriers
 constexpr int kRing = 3;              // pages of K/V in flight per wave
 constexpr int kMaxVerifyQueries = 16; // queries per sequence of a verify call
 // Running-max floor: finite, below any score, so a column that sees no key
@@ -85,7 +93,9 @@ struct DecodeArgs {
   int32_t B, H, G, gchunks, kvg;
   int32_t nkv;       // kv heads
   int32_t nq;        // query tokens per sequence (1 for decode)
-  int32_t nwk;       // waves launched per kv-head group
+  int32_t nwk;       // waves launched per kv-head group (slices)
+  int32_t wgw;       // waves per workgroup: kv groups sharing a slice, a divisor of kvg
+  int32_t wgc;       // workgroups per slice: kvg / wgw
   int32_t max_ctx;   // context bound: min(max_context, block-table width * 16)
   float scale_log2;
 };
@@ -122,27 +132,53 @@ __device__ __forceinline__ int slice_owner(int x, int nw, int total) {
   return static_cast<int>((static_cast<int64_t>(x + 1) * nw - 1) / total);
 }
 
-// Exclusive prefix sum of per-sequence page counts into pre[0..B], by one wave.
+// Exclusive prefix sum of per-sequence page counts into pre[0..B], by the
+// workgroup's first wave; every wave of the workgroup reads it after the
+// barrier.
 __device__ void page_prefix(const DecodeArgs& a, int* pre) {
-  const int lane = threadIdx.x;
-  const int per = (a.B + 63) / 64;
-  const int lo = min(lane * per, a.B);
-  const int hi = min(lo + per, a.B);
-  int s = 0;
-  for (int i = lo; i < hi; ++i) s += pages_of(a, i);
-  int incl = s;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int per = (a.B + 63) / 64;
+    const int lo = min(lane * per, a.B);
+    const int hi = min(lo + per, a.B);
+    int s = 0;
+    for (int i = lo; i < hi; ++i) s += pages_of(a, i);
+    int incl = s;
 #pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int t = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += t;
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(incl, off, 64);
+      if (lane >= off) incl += t;
+    }
+    int run = incl - s;
+    for (int i = lo; i < hi; ++i) {
+      pre[i] = run;
+      run += pages_of(a, i);
+    }
+    if (lo < hi && hi == a.B) pre[a.B] = run;
   }
-  int run = incl - s;
-  for (int i = lo; i < hi; ++i) {
-    pre[i] = run;
-    run += pages_of(a, i);
-  }
-  if (lo < hi && hi == a.B) pre[a.B] = run;
   __syncthreads();
+}
+
+// Slice and first kv group of workgroup w. The wgc workgroups of a slice
+// sit 8 apart, so the dispatcher's round robin over the 8 XCDs puts them on
+// one XCD (its L2 then serves the second column chunk of a verify call the
+// pages the first one fetched), and consecutive slices go to different XCDs.
+__device__ __forceinline__ void wg_slice(const DecodeArgs& a, int w, int* idx, int* kg0) {
+  const int C = a.wgc;
+  const int full = (a.nwk / 8) * 8 * C;  // workgroups in whole groups of 8 slices
+  int r, i;
+  if (w < full) {
+    const int rem = w % (8 * C);
+    r = rem / 8;
+    i = (w / (8 * C)) * 8 + rem % 8;
+  } else {
+    const int t = a.nwk % 8;
+    const int rem = w - full;
+    r = rem / t;
+    i = (a.nwk / 8) * 8 + rem % t;
+  }
+  *idx = i;
+  *kg0 = r * a.wgw;
 }
 
 template <int D>
@@ -170,20 +206,24 @@ __device__ __forceinline__ int v_pos(int r, int c) {
 }
 
 template <int DT, int D>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(
+    DecodeArgs a) {
   constexpr int KK = D / 32;
   constexpr int NN = D / 16;              // 16-row blocks of O^T
   constexpr int LPT = D / 8;              // lanes per token row (16 bytes each)
   constexpr int TPL = 64 / LPT;           // token rows per wave-wide load
   constexpr int VL = PageBuf<D>::VL;
-  __shared__ __attribute__((aligned(16))) uint16_t vb[kPage * D];  // one page of V, rows swizzled
+  __shared__ __attribute__((aligned(16))) uint16_t vbs[kMaxWgWaves][kPage * D];  // per wave: a page of V, swizzled
   extern __shared__ int pre[];  // [B + 1]
 
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x / 64;
+  const int lane = threadIdx.x % 64;
   const int col = lane % 16;
   const int grp = lane / 16;
-  const int kg = blockIdx.x % a.kvg;
-  const int idx = blockIdx.x / a.kvg;
+  uint16_t* const vb = vbs[wave];
+  int idx, kg;
+  wg_slice(a, blockIdx.x, &idx, &kg);
+  kg += wave;
   // Chunk-major: the column chunks of one kv head sit a.nkv blocks apart,
   // on one XCD when a.nkv is a multiple of 8, so a page the first chunk's
   // wave fetches is in that XCD's L2 for the second.
@@ -198,7 +238,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
 
   page_prefix(a, pre);
   const int total = __builtin_amdgcn_readfirstlane(pre[a.B]);
-  if (blockIdx.x == 0) {
+  if (blockIdx.x == 0 && wave == 0) {
     for (int i = lane; i <= a.B; i += 64) a.pre_out[i] = pre[i];
   }
   const int nw = active_waves(total, a.nwk);
@@ -414,6 +454,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void pa
     }
 #pragma unroll
     for (int i = 0; i < kRing + 1; ++i) ref[i] = ref[i + 1];
+    // Every wave of the workgroup has the same lo and hi: all reach each barrier.
+    if ((x - lo) % kSyncPages == kSyncPages - 1) __builtin_amdgcn_s_barrier();
   };
 
   for (int x = lo; x < hi; x += kRing) {
@@ -531,7 +573,7 @@ template <int DT, int D>
 static int launch_decode(const DecodeArgs& a, int phases, hipStream_t stream) {
   if (phases & 1) {
     const size_t dyn = static_cast<size_t>(a.B + 1) * sizeof(int);
-    hipLaunchKernelGGL((paged_decode_kernel<DT, D>), dim3(a.nwk * a.kvg), dim3(64), dyn, stream, a);
+    hipLaunchKernelGGL((paged_decode_kernel<DT, D>), dim3(a.nwk * a.wgc), dim3(64 * a.wgw), dyn, stream, a);
   }
   if (phases & 2) {
     hipLaunchKernelGGL((paged_decode_merge_kernel<DT, D>), dim3(a.B, a.kvg), dim3(kMergeThreads), 0, stream, a);
@@ -637,6 +679,18 @@ static int paged_decode_impl(int phases, int32_t nq, const void* q, int64_t q_st
   // Never more waves per group than the workspace's slots were sized for.
   const int64_t nwk = waves_per_group(cus, a.kvg, max_pages_of(batch, ctx_bound));
   a.nwk = static_cast<int32_t>(nwk);
+  // Kv groups share a workgroup when the launch fills the chip; a shorter
+  // batch keeps one-wave workgroups, spread over every CU.
+  a.wgw = 1;
+  const int64_t resident = cus * kWavesPerCU < kMaxResidentWaves ? cus * kWavesPerCU : kMaxResidentWaves;
+  const bool fills = (nwk + 1) * a.kvg > resident;  // one more wave per group would not fit
+  for (int w = kMaxWgWaves; w > 1 && fills; --w) {
+    if (a.kvg % w == 0) {
+      a.wgw = w;
+      break;
+    }
+  }
+  a.wgc = a.kvg / a.wgw;
   if (nwk * a.kvg > INT32_MAX / 2 || max_pages_of(batch, ctx_bound) > INT32_MAX / 2) return NIMBUS_ERR_UNSUPPORTED;
   const int64_t slots = nwk + batch;
   unsigned char* ws = static_cast<unsigned char*>(workspace);

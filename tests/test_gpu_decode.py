@@ -64,6 +64,25 @@ def test_group_sizes_dtypes_and_long_contexts(dtype, heads, kv, d):
     assert_within(got.cpu(), want, what="vs oracle")
 
 
+@pytest.mark.parametrize("heads,kv,d,batch,max_ctx", [
+    (32, 32, 64, 48, 3000),   # 32 kv groups: 4 workgroups of 8 waves per slice
+    (24, 12, 64, 40, 4000),   # 12 groups: workgroups of 6 waves, 170 slices (a ragged last group of 8)
+    (20, 5, 128, 48, 3000),   # 5 groups: workgroups of 5 waves, 409 slices
+    (32, 2, 128, 16, 8192),   # 2 groups (G = 16): workgroups of 2 waves, 1024 slices
+])
+def test_lockstep_workgroup_shapes(heads, kv, d, batch, max_ctx):
+    """Batches that fill the chip put the kv groups of a slice in one
+    workgroup: every group count (divisors, several workgroups per slice,
+    a slice count that is not a multiple of 8) against the oracle."""
+    announce(f"decode lockstep H={heads} KV={kv} D={d} B={batch}")
+    g = torch.Generator().manual_seed(batch + heads)
+    ctx_lens = [int(c) for c in torch.randint(1, max_ctx + 1, (batch,), generator=g)]
+    ctx_lens[0] = max_ctx
+    q, k, v, ctx, bt, scale = _case(heads, kv, d, ctx_lens, torch.bfloat16, seed=11)
+    got = paged_decode_attention(q, k, v, ctx, bt, max_ctx, scale)
+    assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale), what="vs oracle")
+
+
 def test_grid_width_does_not_change_results():
     """A wider grid (larger max_context, as under graph capture) only adds
     partitions that exit at once: results are bit-identical."""
