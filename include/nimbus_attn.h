@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 9
+#define NIMBUS_ATTN_ABI_VERSION 10
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -267,16 +267,17 @@ int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const void* w_pac
  * nimbus_int8_matmul_packed with an explicit launch plan, for a caller that
  * tunes per shape (as the reference's triton.autotune does per M bucket,
  * N and K): bm tokens per workgroup tile (16, 32 or 64), ks k slices per
- * workgroup (1, 2, 4 or 8, with ks * bm <= 128), splits of K (1..16). Any
- * valid plan gives y to fp32 summation order; the workspace is
+ * workgroup (1, 2, 4 or 8, with ks * bm <= 128), splits of K (1..16) and
+ * rows_per_wave 16-row blocks per wave (1 or 2). Any valid plan gives y to
+ * fp32 summation order; the workspace is
  * nimbus_int8_matmul_packed_plan_workspace_bytes (-1 for an invalid plan).
  */
 int64_t nimbus_int8_matmul_packed_plan_workspace_bytes(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
-                                                       int32_t splits);
+                                                       int32_t splits, int32_t rows_per_wave);
 int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* w_packed, const void* scale, void* y,
                                    int64_t y_stride, int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
-                                   int32_t splits, void* workspace, int64_t workspace_bytes, int32_t dtype,
-                                   void* stream);
+                                   int32_t splits, int32_t rows_per_wave, void* workspace, int64_t workspace_bytes,
+                                   int32_t dtype, void* stream);
 
 /*
  * Rotary position embedding, in place. Replaces Rotary.forward

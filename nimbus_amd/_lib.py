@@ -25,7 +25,7 @@ NIMBUS_ERR_INVALID = -1
 NIMBUS_ERR_UNSUPPORTED = -2
 NIMBUS_ERR_ALIGNMENT = -3
 NIMBUS_ERR_WORKSPACE = -4
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # Entry points and their C signatures, in the order include/nimbus_attn.h declares them.
 _c_int, _c_i32, _c_i64, _c_p, _c_f = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
@@ -60,9 +60,10 @@ SIGNATURES = {
     "nimbus_int8_matmul_packed_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i32]),
     "nimbus_int8_matmul_packed": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p,
                                            _c_i64, _c_i32, _c_p]),
-    "nimbus_int8_matmul_packed_plan_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "nimbus_int8_matmul_packed_plan_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                                _c_i32]),
     "nimbus_int8_matmul_packed_plan": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32,
-                                                _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_p]),
+                                                _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_p]),
     "nimbus_rope": (_c_int, [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_p]),
     "nimbus_silu_mul": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p]),
     "nimbus_greedy_step": (_c_int, [_c_p, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32,

@@ -298,28 +298,31 @@ static int launch_gemm_dt(const GemmArgs& a, hipStream_t s) {
 // row 16 nb + l % 16, k = 64 kc + 16 (l / 16) .. +16 (zero padded), i.e.
 // exactly the A operand one 16-byte load per lane feeds. A wave's weight
 // loads are therefore 1 KB contiguous, and a wave streams one contiguous run
-// of 16 K bytes. The 8 waves of a workgroup are RB row blocks x KS k slices
-// (RB x KS = 8, BM x KS = 128): waves of one row block take interleaved
-// 64-k chunks and their sums are added in LDS at the end (fixed order), so
-// narrow matrices need no cross-workgroup split for small M.
+// of 16 K bytes. The 8 waves of a workgroup are RB row-block groups x KS k
+// slices (RB x KS = 8, BM x KS <= 128); a wave computes RW row blocks (1 or
+// 2) from each x operand it reads. Waves of one group take interleaved 64-k
+// chunks and their sums are added in LDS at the end (fixed order), so narrow
+// matrices need no cross-workgroup split for small M. A step reads all of its
+// x operands from LDS at once and runs its MFMAs on weights converted during
+// the previous step, converting the next step's weights while they execute.
 
 constexpr int kPackRing = 6;  // steps of loads in flight
 
-template <int BM, int KS>
+template <int BM, int KS, int RW>
 struct PackShape {
-  static constexpr int RB = kGemmWaves / KS;                 // row blocks per workgroup
+  static constexpr int RB = kGemmWaves / KS;                 // row-block groups per workgroup
   static constexpr int XP = BM * KS * 8;                     // 16-byte x pieces per step
   static constexpr int XC = (XP + kGemmThreads - 1) / kGemmThreads;  // pieces a thread stages per step
 };
 
-// Grid: (ceil(N / 16 / RB) row tiles, splits, M / BM token tiles).
-template <int DT, int BM, int KS>
+// Grid: (ceil(N / 16 / (RB RW)) row tiles, splits, M / BM token tiles).
+template <int DT, int BM, int KS, int RW>
 __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmArgs a) {
   constexpr int CB = BM / 16;
-  constexpr int RB = PackShape<BM, KS>::RB;
-  constexpr int XP = PackShape<BM, KS>::XP;
-  constexpr int XC = PackShape<BM, KS>::XC;
-  static_assert((KS - 1) * RB * CB * 1024 <= 2 * KS * BM * kXRow, "the k-slice sums fit the x buffers");
+  constexpr int RB = PackShape<BM, KS, RW>::RB;
+  constexpr int XP = PackShape<BM, KS, RW>::XP;
+  constexpr int XC = PackShape<BM, KS, RW>::XC;
+  static_assert((KS - 1) * RB * RW * CB * 1024 <= 2 * KS * BM * kXRow, "the k-slice sums fit the x buffers");
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][KS * BM * kXRow];
 
   const int tid = threadIdx.x;
@@ -331,9 +334,9 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
   const int rb = wave / KS;
   const int nblocks = (a.N + 15) / 16;
   const int kchunks = (a.K + 63) / 64;
-  const int nb = blockIdx.x * RB + rb;
-  const int c0 = blockIdx.y * (a.ksplit / 64);         // first 64-k chunk of this split
-  const int ce = min(kchunks, c0 + a.ksplit / 64);     // chunk end
+  const int nb0 = (blockIdx.x * RB + rb) * RW;
+  const int c0 = blockIdx.y * (a.ksplit / 64);
+  const int ce = min(kchunks, c0 + a.ksplit / 64);
   const int m0 = blockIdx.z * BM;
   const int steps = (ce - c0 + KS - 1) / KS;
 
@@ -341,16 +344,15 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
       const_cast<int8_t*>(a.w), 0, __builtin_amdgcn_readfirstlane(a.w_bytes), kBufferFlags);
   const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(a.x), 0, __builtin_amdgcn_readfirstlane(a.x_bytes), kBufferFlags);
-  // Step s: this wave's chunk is c0 + KS s + ks of row block nb (blocks past
-  // the last read the last one and are never stored).
-  const uint32_t woff = static_cast<uint32_t>((min(nb, nblocks - 1) * kchunks + c0 + ks) * 1024 + 16 * lane);
-  auto load_w = [&](int s) {
+  uint32_t woff[RW];
+#pragma unroll
+  for (int j = 0; j < RW; ++j)
+    woff[j] = static_cast<uint32_t>((min(nb0 + j, nblocks - 1) * kchunks + c0 + ks) * 1024 + 16 * lane);
+  auto load_w = [&](int s, int j) {
     const bool on = c0 + KS * s + ks < ce;
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                         wrsrc, on ? woff + KS * 1024 * s : kOutOfRange, 0, 0));
+                                         wrsrc, on ? woff[j] + KS * 1024 * s : kOutOfRange, 0, 0));
   };
-  // x: piece q = tid + 512 i (< XP) of a step is chunk j = q / (8 BM) of the
-  // step, token (q % (8 BM)) / 8, elements 8 (q % 8) .. +8.
   uint32_t xoff[XC];
   int xk[XC], xs_off[XC];
   bool x_on[XC], x_mine[XC];
@@ -379,96 +381,123 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
     }
   };
 
-  u32x4 wr[kPackRing], xr[kPackRing][XC];
+  u32x4 wr[kPackRing][RW], xr[kPackRing][XC];
 #pragma unroll
   for (int r = 0; r < kPackRing; ++r) {
-    wr[r] = load_w(r);
+#pragma unroll
+    for (int j = 0; j < RW; ++j) wr[r][j] = load_w(r, j);
 #pragma unroll
     for (int i = 0; i < XC; ++i) xr[r][i] = load_x(r, i);
   }
   stage_x(0, xr[0]);
-  lds_barrier();
 
-  f32x4 acc[CB];
+  f32x4 acc[RW][CB];
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb) acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < RW; ++j)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) acc[j][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int xb_off = (ks * BM + col) * kXRow + 32 * grp;
 
-  // One step: consume ring slot r (step s), optionally refill it with step
-  // s + kPackRing, stage x(s + 1), barrier.
-  auto step = [&](int s, int r, bool refill, u32x4& wslot, u32x4* xslot, const u32x4* xnext) {
-    const uint8_t* xb = &xs[s & 1][xb_off];
-    const u32x4 a0 = i8x8_to_operand<DT>(wslot[0], wslot[1]);
-    const u32x4 a1 = i8x8_to_operand<DT>(wslot[2], wslot[3]);
-    if (refill) {
-      wslot = load_w(s + kPackRing);
+  // Weights of the step about to run, already in operand form.
+  u32x4 a0[RW], a1[RW];
 #pragma unroll
-      for (int i = 0; i < XC; ++i) xslot[i] = load_x(s + kPackRing, i);
-      __builtin_amdgcn_sched_barrier(0);  // issue the refill now, not after this step's MFMAs
-    }
+  for (int j = 0; j < RW; ++j) {
+    a0[j] = i8x8_to_operand<DT>(wr[0][j][0], wr[0][j][1]);
+    a1[j] = i8x8_to_operand<DT>(wr[0][j][2], wr[0][j][3]);
+  }
+  lds_barrier();
+
+  // One step s (ring slot r): read all of x(s) from LDS, refill slot r with
+  // step s + kPackRing, run the MFMAs on the weights converted last step,
+  // convert step s + 1's weights while they run, stage x(s + 1), barrier.
+  auto step = [&](int s, bool refill, u32x4* wslot, u32x4* xslot, const u32x4* wnext, const u32x4* xnext) {
+    const uint8_t* xb = &xs[s & 1][xb_off];
+    u32x4 b0[CB], b1[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
-      const u32x4 b0 = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow);
-      const u32x4 b1 = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow + 16);
-      acc[cb] = mfma_16x16x32<DT>(a0, b0, acc[cb]);
-      acc[cb] = mfma_16x16x32<DT>(a1, b1, acc[cb]);
+      b0[cb] = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow);
+      b1[cb] = *reinterpret_cast<const u32x4*>(xb + cb * 16 * kXRow + 16);
+    }
+    if (refill) {
+#pragma unroll
+      for (int j = 0; j < RW; ++j) wslot[j] = load_w(s + kPackRing, j);
+#pragma unroll
+      for (int i = 0; i < XC; ++i) xslot[i] = load_x(s + kPackRing, i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+#pragma unroll
+      for (int j = 0; j < RW; ++j) {
+        acc[j][cb] = mfma_16x16x32<DT>(a0[j], b0[cb], acc[j][cb]);
+        acc[j][cb] = mfma_16x16x32<DT>(a1[j], b1[cb], acc[j][cb]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < RW; ++j) {
+      a0[j] = i8x8_to_operand<DT>(wnext[j][0], wnext[j][1]);
+      a1[j] = i8x8_to_operand<DT>(wnext[j][2], wnext[j][3]);
     }
     stage_x((s + 1) & 1, xnext);
     lds_barrier();
   };
 
-  // Whole rings with refills, then the remaining steps without (the ring's
-  // registers keep their places; no step past the range is computed).
   int s0 = 0;
   for (; s0 + kPackRing <= steps; s0 += kPackRing) {
 #pragma unroll
-    for (int r = 0; r < kPackRing; ++r) step(s0 + r, r, true, wr[r], xr[r], xr[(r + 1) % kPackRing]);
+    for (int r = 0; r < kPackRing; ++r)
+      step(s0 + r, true, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 1) % kPackRing]);
   }
 #pragma unroll
   for (int r = 0; r < kPackRing; ++r) {
-    if (s0 + r < steps) step(s0 + r, r, false, wr[r], xr[r], xr[(r + 1) % kPackRing]);
+    if (s0 + r < steps) step(s0 + r, false, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 1) % kPackRing]);
   }
 
-  // Sum the KS k slices of each row block in slice order (LDS reuses the x
-  // buffers: every wave passed the last barrier).
   if constexpr (KS > 1) {
-    f32x4* red = reinterpret_cast<f32x4*>(&xs[0][0]);  // [KS - 1][RB][CB][64 lanes]
+    f32x4* red = reinterpret_cast<f32x4*>(&xs[0][0]);  // [KS - 1][RB][RW][CB][64 lanes]
     if (ks > 0) {
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) red[(((ks - 1) * RB + rb) * CB + cb) * 64 + lane] = acc[cb];
+      for (int j = 0; j < RW; ++j)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) red[((((ks - 1) * RB + rb) * RW + j) * CB + cb) * 64 + lane] = acc[j][cb];
     }
     lds_barrier();
     if (ks > 0) return;
 #pragma unroll
-    for (int j = 1; j < KS; ++j) {
+    for (int t = 1; t < KS; ++t) {
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) acc[cb] += red[(((j - 1) * RB + rb) * CB + cb) * 64 + lane];
+      for (int j = 0; j < RW; ++j)
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[j][cb] += red[((((t - 1) * RB + rb) * RW + j) * CB + cb) * 64 + lane];
     }
   }
 
-  const int n = 16 * nb + 4 * grp;
-  if (n >= a.N) return;
-  if (a.splits == 1) {
-    const u32x2 sw = *reinterpret_cast<const u32x2*>(a.scale + n);
-    const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
-                         Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const int m = m0 + 16 * cb + col;
-      if (m < a.M) {
-        const f32x4 o = acc[cb];
-        const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(o[0] * sc[0]), Elem<DT>::from_f32(o[1] * sc[1])),
-                              pack2(Elem<DT>::from_f32(o[2] * sc[2]), Elem<DT>::from_f32(o[3] * sc[3]))};
-        *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
+  for (int j = 0; j < RW; ++j) {
+    const int n = 16 * (nb0 + j) + 4 * grp;
+    if (n >= a.N) continue;
+    if (a.splits == 1) {
+      const u32x2 sw = *reinterpret_cast<const u32x2*>(a.scale + n);
+      const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
+                           Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int m = m0 + 16 * cb + col;
+        if (m < a.M) {
+          const f32x4 o = acc[j][cb];
+          const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(o[0] * sc[0]), Elem<DT>::from_f32(o[1] * sc[1])),
+                                pack2(Elem<DT>::from_f32(o[2] * sc[2]), Elem<DT>::from_f32(o[3] * sc[3]))};
+          *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
+        }
       }
-    }
-  } else {
+    } else {
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const int m = m0 + 16 * cb + col;
-      if (m < a.M) {
-        float* p = a.part + (static_cast<int64_t>(blockIdx.y) * a.M + m) * a.N + n;
-        *reinterpret_cast<f32x4*>(p) = acc[cb];
+      for (int cb = 0; cb < CB; ++cb) {
+        const int m = m0 + 16 * cb + col;
+        if (m < a.M) {
+          float* p = a.part + (static_cast<int64_t>(blockIdx.y) * a.M + m) * a.N + n;
+          *reinterpret_cast<f32x4*>(p) = acc[j][cb];
+        }
       }
     }
   }
@@ -510,13 +539,14 @@ static int64_t packed_bytes(int32_t n, int32_t k) {
 // splits if the row tiles alone still leave CUs idle. A pure function of
 // the shape.
 struct PackPlan {
-  int bm, ks;
+  int bm, ks, rw;
   int32_t splits, ksplit;
 };
 
 static PackPlan packed_plan(int64_t m, int32_t n, int32_t k) {
   PackPlan p;
   p.bm = gemm_bm(m);
+  p.rw = 1;
   const int64_t nblocks = (n + 15) / 16;
   const int64_t mtiles = (m + p.bm - 1) / p.bm;
   const int max_ks = kGemmWaves * 16 / p.bm;  // 16 RB >= BM
@@ -544,11 +574,11 @@ static PackPlan packed_plan(int64_t m, int32_t n, int32_t k) {
   return p;
 }
 
-template <int DT, int BM, int KS>
+template <int DT, int BM, int KS, int RW>
 static int launch_packed(const GemmArgs& a, hipStream_t s) {
-  constexpr int RB = PackShape<BM, KS>::RB;
-  const dim3 grid(((a.N + 15) / 16 + RB - 1) / RB, a.splits, (a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((int8_matmul_packed_kernel<DT, BM, KS>), grid, dim3(kGemmThreads), 0, s, a);
+  constexpr int RB = PackShape<BM, KS, RW>::RB;
+  const dim3 grid(((a.N + 15) / 16 + RB * RW - 1) / (RB * RW), a.splits, (a.M + BM - 1) / BM);
+  hipLaunchKernelGGL((int8_matmul_packed_kernel<DT, BM, KS, RW>), grid, dim3(kGemmThreads), 0, s, a);
   if (a.splits > 1) {
     const int64_t quads = static_cast<int64_t>(a.M) * (a.N / 4);
     hipLaunchKernelGGL((int8_matmul_reduce_kernel<DT>), dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256),
@@ -557,22 +587,27 @@ static int launch_packed(const GemmArgs& a, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
+template <int DT, int BM, int KS>
+static int launch_packed_rw(const GemmArgs& a, int rw, hipStream_t s) {
+  return rw == 2 ? launch_packed<DT, BM, KS, 2>(a, s) : launch_packed<DT, BM, KS, 1>(a, s);
+}
+
 template <int DT, int BM>
-static int launch_packed_bm(const GemmArgs& a, int ks, hipStream_t s) {
+static int launch_packed_bm(const GemmArgs& a, int ks, int rw, hipStream_t s) {
   switch (ks) {
-    case 1: return launch_packed<DT, BM, 1>(a, s);
-    case 2: return launch_packed<DT, BM, 2>(a, s);
-    case 4: if constexpr (BM <= 32) return launch_packed<DT, BM, 4>(a, s); else return NIMBUS_ERR_UNSUPPORTED;
-    default: if constexpr (BM <= 16) return launch_packed<DT, BM, 8>(a, s); else return NIMBUS_ERR_UNSUPPORTED;
+    case 1: return launch_packed_rw<DT, BM, 1>(a, rw, s);
+    case 2: return launch_packed_rw<DT, BM, 2>(a, rw, s);
+    case 4: if constexpr (BM <= 32) return launch_packed_rw<DT, BM, 4>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
+    default: if constexpr (BM <= 16) return launch_packed_rw<DT, BM, 8>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
   }
 }
 
 template <int DT>
 static int launch_packed_dt(const GemmArgs& a, const PackPlan& p, hipStream_t s) {
   switch (p.bm) {
-    case 16: return launch_packed_bm<DT, 16>(a, p.ks, s);
-    case 32: return launch_packed_bm<DT, 32>(a, p.ks, s);
-    default: return launch_packed_bm<DT, 64>(a, p.ks, s);
+    case 16: return launch_packed_bm<DT, 16>(a, p.ks, p.rw, s);
+    case 32: return launch_packed_bm<DT, 32>(a, p.ks, p.rw, s);
+    default: return launch_packed_bm<DT, 64>(a, p.ks, p.rw, s);
   }
 }
 
@@ -700,13 +735,16 @@ extern "C" int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const 
 }
 
 // An explicit plan: token tile bm (16, 32, 64), k slices ks (1, 2, 4, 8;
-// ks * bm <= 128) and k splits (1..16, fewer when K is short). Workspace:
-// splits * m * n * 4 bytes when the plan splits.
-static bool make_plan(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks, int32_t splits, PackPlan* p) {
+// ks * bm <= 128), k splits (1..16, fewer when K is short) and row blocks
+// per wave rw (1, 2). Workspace: splits * m * n * 4 bytes when the plan
+// splits.
+static bool make_plan(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks, int32_t splits, int32_t rw,
+                      PackPlan* p) {
   (void)m;
   (void)n;
   if (bm != 16 && bm != 32 && bm != 64) return false;
   if (ks != 1 && ks != 2 && ks != 4 && ks != 8) return false;
+  if (rw != 1 && rw != 2) return false;
   if (ks * bm > 128 || splits < 1 || splits > kMaxSplits) return false;
   const int64_t step_k = 64 * ks;
   const int64_t kp = (k + 63) / 64 * 64;
@@ -714,25 +752,28 @@ static bool make_plan(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks, i
   ksp = (ksp + step_k - 1) / step_k * step_k;
   p->bm = bm;
   p->ks = ks;
+  p->rw = rw;
   p->ksplit = static_cast<int32_t>(ksp);
   p->splits = static_cast<int32_t>((kp + ksp - 1) / ksp);
   return true;
 }
 
 extern "C" int64_t nimbus_int8_matmul_packed_plan_workspace_bytes(int64_t m, int32_t n, int32_t k, int32_t bm,
-                                                                  int32_t ks, int32_t splits) {
+                                                                  int32_t ks, int32_t splits,
+                                                                  int32_t rows_per_wave) {
   PackPlan p;
-  if (m < 0 || n <= 0 || k <= 0 || !make_plan(m, n, k, bm, ks, splits, &p)) return -1;
+  if (m < 0 || n <= 0 || k <= 0 || !make_plan(m, n, k, bm, ks, splits, rows_per_wave, &p)) return -1;
   return p.splits > 1 ? static_cast<int64_t>(p.splits) * m * n * 4 : 0;
 }
 
 extern "C" int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* w_packed,
                                               const void* scale, void* y, int64_t y_stride, int64_t m, int32_t n,
-                                              int32_t k, int32_t bm, int32_t ks, int32_t splits, void* workspace,
-                                              int64_t workspace_bytes, int32_t dtype, void* stream) {
+                                              int32_t k, int32_t bm, int32_t ks, int32_t splits,
+                                              int32_t rows_per_wave, void* workspace, int64_t workspace_bytes,
+                                              int32_t dtype, void* stream) {
   PackPlan p;
   if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
-  if (!make_plan(m, n, k, bm, ks, splits, &p)) return NIMBUS_ERR_UNSUPPORTED;
+  if (!make_plan(m, n, k, bm, ks, splits, rows_per_wave, &p)) return NIMBUS_ERR_UNSUPPORTED;
   return packed_impl(x, x_stride, w_packed, scale, y, y_stride, m, n, k, &p, workspace, workspace_bytes, dtype,
                      stream);
 }

@@ -100,14 +100,14 @@ def unpack_int8_weight(packed: torch.Tensor, n: int, k: int) -> torch.Tensor:
     return t.permute(0, 3, 1, 2, 4).reshape(nb * 16, kc * 64)[:n, :k].contiguous()
 
 
-# Launch plans (token tile, k slices, K splits) tuned per (M bucket, N, K,
+# Launch plans (token tile, k slices, K splits, row blocks per wave) tuned per (M bucket, N, K,
 # dtype, device), as nimbus/kernels/int8_matmul.py:16-24 autotunes its
 # Triton configs per M bucket. Tuning times every candidate plan on the
 # call's own inputs, eagerly, the first time a key is seen; a call being
 # captured into a graph never tunes and uses the tuned plan or the
 # library's default. Set AUTOTUNE = False to always use the default.
 AUTOTUNE = True
-_TUNED: dict[tuple, tuple[int, int, int] | None] = {}
+_TUNED: dict[tuple, tuple[int, int, int, int] | None] = {}
 _TUNE_BYTES = 600e6  # weight copies the timing rotates over (beyond the 256 MB Infinity Cache)
 
 
@@ -116,7 +116,7 @@ def m_bucket(m: int) -> int:
     return 1 << max(4, (m - 1).bit_length()) if m <= 256 else 512
 
 
-def _candidate_plans(m: int, n: int, k: int) -> list[tuple[int, int, int]]:
+def _candidate_plans(m: int, n: int, k: int) -> list[tuple[int, int, int, int]]:
     nb = -(-n // 16)
     plans = []
     for bm in (16, 32, 64):
@@ -125,16 +125,19 @@ def _candidate_plans(m: int, n: int, k: int) -> list[tuple[int, int, int]]:
         for ks in (1, 2, 4, 8):
             if ks * bm > 128:
                 continue
-            tiles = -(-nb // (8 // ks)) * -(-m // bm)
-            for splits in (1, 2, 3, 4, 6, 8, 12, 16):
-                if splits > 1 and k < 4 * 64 * ks * splits:
-                    continue
-                if 64 <= tiles * splits <= 768:
-                    plans.append((bm, ks, splits))
+            for rw in (1, 2):
+                if rw > 1 and m <= 16:
+                    continue  # two row blocks per x read pay only when x is read for many tokens
+                tiles = -(-nb // (8 // ks * rw)) * -(-m // bm)
+                for splits in (1, 2, 3, 4, 6, 8, 12, 16):
+                    if splits > 1 and k < 4 * 64 * ks * splits:
+                        continue
+                    if 64 <= tiles * splits <= 768:
+                        plans.append((bm, ks, splits, rw))
     return plans
 
 
-def _tune(x2, w_packed, scale, y, n, k, lib) -> tuple[int, int, int] | None:
+def _tune(x2, w_packed, scale, y, n, k, lib) -> tuple[int, int, int, int] | None:
     m = x2.shape[0]
     plans = _candidate_plans(m, n, k)
     if len(plans) < 2:

@@ -193,6 +193,16 @@ def test_int8_workspace_is_splits_times_fp32_output():
     assert ws(1, 3072, 2048) == 4 * 1 * 3072 * 4  # 24 tiles want 11 splits; 2048 / 512 allows 4
 
 
+def test_int8_explicit_plan_workspace_and_validation():
+    lib = _lib.load()
+    ws = lib.nimbus_int8_matmul_packed_plan_workspace_bytes
+    assert ws(64, 4096, 14336, 64, 2, 4, 1) == 4 * 64 * 4096 * 4
+    assert ws(64, 4096, 14336, 32, 2, 4, 2) == 4 * 64 * 4096 * 4  # rows per wave does not change the split
+    assert ws(64, 28672, 4096, 64, 2, 1, 2) == 0
+    for bad in [(48, 1, 1, 1), (64, 4, 1, 1), (16, 3, 1, 1), (16, 1, 17, 1), (16, 1, 1, 0), (16, 1, 1, 3)]:
+        assert ws(64, 4096, 4096, *bad) == -1, bad
+
+
 def test_prefill_pieces_checks():
     lib = _lib.load()
     assert lib.nimbus_paged_prefill_pieces_workspace_bytes(3, 32, 128) == 3 * 64 * 32 * 130 * 4

@@ -150,7 +150,8 @@ def test_pack_unpack_roundtrip_and_layout(n, k):
 
 @pytest.mark.parametrize("m,n,k", [(33, 4100, 1040), (64, 4096, 4096), (7, 6144, 4096), (1, 260, 8192)])
 def test_every_launch_plan_is_exact(m, n, k):
-    """Each plan the tuner may pick (token tile, k slices, K splits) gives
+    """Each plan the tuner may pick (token tile, k slices, K splits, row
+    blocks per wave) gives
     the float64 product rounded once on integer inputs, so tuning can only
     change speed."""
     from nimbus_amd import _lib
