@@ -304,7 +304,8 @@ static int launch_gemm_dt(const GemmArgs& a, hipStream_t s) {
 // chunks and their sums are added in LDS at the end (fixed order), so narrow
 // matrices need no cross-workgroup split for small M. A step reads all of its
 // x operands from LDS at once and runs its MFMAs on weights converted during
-// the previous step, converting the next step's weights while they execute.
+// the previous step, converting the next step's weights while they execute;
+// the workgroup meets at a barrier every second step.
 
 constexpr int kPackRing = 6;  // steps of loads in flight
 
@@ -322,8 +323,10 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
   constexpr int RB = PackShape<BM, KS, RW>::RB;
   constexpr int XP = PackShape<BM, KS, RW>::XP;
   constexpr int XC = PackShape<BM, KS, RW>::XC;
-  static_assert((KS - 1) * RB * RW * CB * 1024 <= 2 * KS * BM * kXRow, "the k-slice sums fit the x buffers");
-  __shared__ __attribute__((aligned(16))) uint8_t xs[2][KS * BM * kXRow];
+  static_assert((KS - 1) * RB * RW * CB * 1024 <= 4 * KS * BM * kXRow, "the k-slice sums fit the x buffers");
+  // Four x buffers: step s reads buffer s % 4 and stages x(s + 2), so one
+  // barrier every second step keeps writers off buffers still being read.
+  __shared__ __attribute__((aligned(16))) uint8_t xs[4][KS * BM * kXRow];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
@@ -390,6 +393,7 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
     for (int i = 0; i < XC; ++i) xr[r][i] = load_x(r, i);
   }
   stage_x(0, xr[0]);
+  stage_x(1, xr[1]);
 
   f32x4 acc[RW][CB];
 #pragma unroll
@@ -409,9 +413,11 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
 
   // One step s (ring slot r): read all of x(s) from LDS, refill slot r with
   // step s + kPackRing, run the MFMAs on the weights converted last step,
-  // convert step s + 1's weights while they run, stage x(s + 1), barrier.
+  // convert step s + 1's weights while they run, stage x(s + 2), and meet the
+  // other waves after odd steps (x(s + 2) goes to the buffer step s - 2 read,
+  // and every wave has passed the barrier after step s - 1).
   auto step = [&](int s, bool refill, u32x4* wslot, u32x4* xslot, const u32x4* wnext, const u32x4* xnext) {
-    const uint8_t* xb = &xs[s & 1][xb_off];
+    const uint8_t* xb = &xs[s & 3][xb_off];
     u32x4 b0[CB], b1[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
@@ -438,20 +444,21 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
       a0[j] = i8x8_to_operand<DT>(wnext[j][0], wnext[j][1]);
       a1[j] = i8x8_to_operand<DT>(wnext[j][2], wnext[j][3]);
     }
-    stage_x((s + 1) & 1, xnext);
-    lds_barrier();
+    stage_x((s + 2) & 3, xnext);
+    if (s & 1) lds_barrier();
   };
 
   int s0 = 0;
   for (; s0 + kPackRing <= steps; s0 += kPackRing) {
 #pragma unroll
     for (int r = 0; r < kPackRing; ++r)
-      step(s0 + r, true, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 1) % kPackRing]);
+      step(s0 + r, true, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 2) % kPackRing]);
   }
 #pragma unroll
   for (int r = 0; r < kPackRing; ++r) {
-    if (s0 + r < steps) step(s0 + r, false, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 1) % kPackRing]);
+    if (s0 + r < steps) step(s0 + r, false, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 2) % kPackRing]);
   }
+  if (steps & 1) lds_barrier();  // the last step read x: before LDS is reused below
 
   if constexpr (KS > 1) {
     f32x4* red = reinterpret_cast<f32x4*>(&xs[0][0]);  // [KS - 1][RB][RW][CB][64 lanes]
