@@ -12,16 +12,18 @@ value        algorithmic bytes of one call / wall time per step (GB/s):
              every visible K and V row once, q and out once, the page ids and
              context lengths (nimbus_amd.workloads.decode_bytes)
 roofline     the page pass (paged_decode_kernel, the dominant kernel) alone,
-             timed with HIP events on the launch stream: algorithmic bytes /
-             its mean duration, against 8 TB/s; `traffic` is the HBM bytes
+             K launches back to back between one HIP event pair on the launch
+             stream: algorithmic bytes / mean duration per launch, against
+             8 TB/s (`kernel_us_event_pairs`: the mean with an event pair
+             around each launch, which adds its dispatch latency); `traffic` is the HBM bytes
              per launch that rocprofv3 FETCH_SIZE + WRITE_SIZE measured for
              this kernel and workload (profiles/decode_llama3_traffic.json,
              scaled by the plain-copy calibration), null when absent
 cpu_baseline the CPU oracle (restated nimbus/kernels/reference.py:71-96,
              batched exact form) on this host's cores, same inputs
 prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
-             prefixes of up to 1024): causal FLOPs / mean kernel time, against
-             the 2.5 PFLOP/s dense bf16 MFMA peak
+             prefixes of up to 1024): causal FLOPs / mean time per call of K
+             back-to-back calls, against the 2.5 PFLOP/s dense bf16 MFMA peak
 mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
              (eager) + the 60 decodes replayed from a hipGraph padded to 64
 verify       speculative verification's attention (16 sequences x 5 tokens)
@@ -113,6 +115,21 @@ def measured_traffic(kernel, algorithmic_bytes):
 
 # ---------------------------------------------------------------- timing helpers
 
+def region_us(fn, steps, stream):
+    """Runs fn(i) for i < steps back to back between one HIP event pair on
+    `stream`; returns the mean time per call in microseconds (each launch's
+    duration plus the gap to the next one, as a stream of calls sees it)."""
+    import torch
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for i in range(steps):
+        fn(i)
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) * 1e3 / steps
+
+
 def event_times_us(fn, steps, stream):
     """Runs fn(i) for i < steps with a HIP event pair around each call on
     `stream`; returns the per-call durations in microseconds."""
@@ -176,10 +193,14 @@ def time_decode(batch, steps, warmup, wall=True):
             call(i)
         torch.cuda.synchronize()
         res["ms_per_step"] = (time.perf_counter() - w0) * 1e3 / steps
-    res["call_us"] = statistics.mean(event_times_us(call, steps, stream))
-    res["page_pass_us"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_pages"),
-                                                         steps, stream))
-    res["merge_us"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_merge"), steps, stream))
+    res["call_us"] = region_us(call, steps, stream)
+    res["page_pass_us"] = region_us(lambda i: call(i, "nimbus_paged_decode_pages"), steps, stream)
+    # the same with an event pair around each call (adds each launch's own dispatch latency)
+    res["call_us_event_pairs"] = statistics.mean(event_times_us(call, steps, stream))
+    res["page_pass_us_event_pairs"] = statistics.mean(event_times_us(lambda i: call(i, "nimbus_paged_decode_pages"),
+                                                                     steps, stream))
+    # the merge pass's share of a call (timed alone, a 5 us launch is bound by the host's launch rate)
+    res["merge_us"] = res["call_us"] - res["page_pass_us"]
     res["bytes"] = workloads.decode_bytes(ctx_lens, h, kv, d, batch.q.element_size())
     res["pools"] = len(pools)
     res["batch"] = b
@@ -255,11 +276,13 @@ def time_prefill(batch, steps, warmup):
 
     for i in range(warmup):
         call(i)
-    us = statistics.mean(event_times_us(call, steps, torch.cuda.current_stream()))
+    us = region_us(call, steps, torch.cuda.current_stream())
+    us_pairs = statistics.mean(event_times_us(call, steps, torch.cuda.current_stream()))
     seqs = batch.seqs[:batch.num_prefills]
     h, d = batch.q.shape[1], batch.q.shape[2]
     flops = workloads.prefill_flops(seqs, h, d)
-    return {"us_per_call": us, "flops": flops, "tflops": flops / us / 1e6, "tiles": int(progs[0].numel())}
+    return {"us_per_call": us, "us_per_call_event_pairs": us_pairs, "flops": flops, "tflops": flops / us / 1e6,
+            "tiles": int(progs[0].numel())}
 
 
 def time_mixed_step(batch, steps, warmup):
@@ -648,7 +671,8 @@ def main(argv=None):
             "frac": part_gbs / HBM_PEAK_GBS,
             "traffic": measured_traffic("paged_decode_kernel", dec["bytes"]),
             "kernel_us": dec["page_pass_us"],
-            "merge_pass_us": dec["merge_us"],
+            "kernel_us_event_pairs": dec["page_pass_us_event_pairs"],
+            "merge_pass_share_us": dec["merge_us"],
         },
     }
     if not args.no_prefill:
