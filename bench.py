@@ -42,6 +42,9 @@ int8_matmul  the INT8 weight-only matmul at Llama-3-8B decode projections
 
 Between timed calls the K/V pool rotates over enough copies (>= 1.5 GB) that
 the 256 MB Infinity Cache cannot serve one call's pages to the next.
+other_configs BASELINE configs 1, 2 and 5 in compact form (at most 50
+             timed calls each)
+
 --all also times every BASELINE config and writes gpurun_out/bench_configs.json.
 """
 
@@ -580,6 +583,40 @@ def time_decode_step(steps, warmup, chain=16):
     return res
 
 
+# ---------------------------------------------------------------- configs 1, 2 and 5
+
+def other_configs(steps, warmup):
+    """BASELINE configs 1 (TinyLlama decode), 2 (TinyLlama varlen prefill)
+    and 5 (long-context decode, ~40 GB pool) in compact form: µs per call of
+    back-to-back calls, GB/s or TFLOP/s and the roofline fraction."""
+    import torch
+
+    from nimbus_amd import workloads
+
+    rows = {}
+    for cfg, name in ((1, "tinyllama_decode"), (5, "llama3_long_decode")):
+        log(f"config {cfg} ({name})")
+        b = workloads.CONFIGS[name]("cuda")
+        r = time_decode(b, steps, warmup, wall=False)
+        rows[f"config{cfg}"] = {
+            "workload": name, "batch": r["batch"], "sum_ctx": r["sum_ctx"], "bytes": r["bytes"],
+            "us_per_call": r["call_us"], "page_pass_us": r["page_pass_us"],
+            "GBps_call": r["bytes"] / r["call_us"] / 1e3,
+            "frac_hbm_peak_call": r["bytes"] / r["call_us"] / 1e3 / HBM_PEAK_GBS,
+            "frac_hbm_peak_page_pass": r["bytes"] / r["page_pass_us"] / 1e3 / HBM_PEAK_GBS,
+        }
+        del b
+        torch.cuda.empty_cache()
+    log("config 2 (tinyllama_prefill)")
+    b = workloads.CONFIGS["tinyllama_prefill"]("cuda")
+    r = time_prefill(b, steps, warmup)
+    rows["config2"] = {"workload": "tinyllama_prefill", "us_per_call": r["us_per_call"], "flops": r["flops"],
+                       "tflops": r["tflops"], "frac_mfma_peak": r["tflops"] / MFMA_BF16_PEAK_TFLOPS}
+    del b
+    torch.cuda.empty_cache()
+    return rows
+
+
 # ---------------------------------------------------------------- --all
 
 def all_configs(steps, warmup):
@@ -698,6 +735,8 @@ def main(argv=None):
         log("decode_step (whole model)")
         result["decode_step"] = time_decode_step(args.steps, args.warmup)
         log(f"decode_step: {result['decode_step']}")
+    if not args.no_prefill:
+        result["other_configs"] = other_configs(min(args.steps, 50), args.warmup)
     if args.all:
         result["configs"] = {k: {a: b for a, b in v.items() if not isinstance(b, dict)}
                              for k, v in all_configs(args.steps, args.warmup).items()}
