@@ -410,13 +410,18 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     mask_and_max(sa, kbeg);
     __syncthreads();
   }
-  auto iteration = [&](int kb, auto slot, auto has_k2, auto has_next, Scores& s_cur, Scores& s_nxt) {
+  // Two forms of the iteration: with the next block (all but the last) and
+  // the last one. The first form always issues K(kb + 2): past the context
+  // it reads zeros through an empty buffer resource, past a piece's range it
+  // is loaded and never read. So the walk inlines five copies of the
+  // iteration in two forms instead of one per tail length and form, which
+  // keeps the tail inside the register budget.
+  auto iteration = [&](int kb, auto slot, auto has_next, Scores& s_cur, Scores& s_nxt) {
     constexpr int SLOT = decltype(slot)::value;
-    constexpr bool K2 = decltype(has_k2)::value;
     constexpr bool NEXT = decltype(has_next)::value;
     BlockPages pg_n;
-    if constexpr (NEXT) issue_v(pg_v, kb + 1);
-    if constexpr (K2) {
+    if constexpr (NEXT) {
+      issue_v(pg_v, kb + 1);
       pg_n = load_pages(kb + 3);
       dma_k(pg_k, kb + 2, IntC<SLOT>{});
     }
@@ -436,26 +441,25 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
       store_v(IntC<1 - SLOT>{});
       mask_and_max(s_nxt, kb + 1);
       __syncthreads();
+      pg_v = pg_k;
+      pg_k = pg_n;
     }
-    pg_v = pg_k;
-    if constexpr (K2) pg_k = pg_n;
   };
   int kb = kbeg;
-  for (; kb + 3 < kend; kb += 2) {
-    iteration(kb, IntC<0>{}, BoolC<true>{}, BoolC<true>{}, sa, sb);
-    iteration(kb + 1, IntC<1>{}, BoolC<true>{}, BoolC<true>{}, sb, sa);
+  for (; kb + 2 < kend; kb += 2) {
+    iteration(kb, IntC<0>{}, BoolC<true>{}, sa, sb);
+    iteration(kb + 1, IntC<1>{}, BoolC<true>{}, sb, sa);
   }
-  // kb - kbeg is even here; 0 to 3 iterations remain.
-  if (kb + 2 < kend) {
-    iteration(kb, IntC<0>{}, BoolC<true>{}, BoolC<true>{}, sa, sb);
-    iteration(kb + 1, IntC<1>{}, BoolC<false>{}, BoolC<true>{}, sb, sa);
-    iteration(kb + 2, IntC<0>{}, BoolC<false>{}, BoolC<false>{}, sa, sb);
-  } else if (kb + 1 < kend) {
-    iteration(kb, IntC<0>{}, BoolC<false>{}, BoolC<true>{}, sa, sb);
-    iteration(kb + 1, IntC<1>{}, BoolC<false>{}, BoolC<false>{}, sb, sa);
+  // kb - kbeg is even here; one or two iterations remain.
+  if (kb + 1 < kend) {
+    iteration(kb, IntC<0>{}, BoolC<true>{}, sa, sb);
+    iteration(kb + 1, IntC<1>{}, BoolC<false>{}, sb, sa);
   } else if (kb < kend) {
-    iteration(kb, IntC<0>{}, BoolC<false>{}, BoolC<false>{}, sa, sb);
+    iteration(kb, IntC<0>{}, BoolC<false>{}, sa, sb);
   }
+  // The last K copies issued may still be in flight (into a slot nothing
+  // reads any more); let them land before the workgroup's LDS is released.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   if (slot >= 0) {
     if (slot >= a.slots) return;
