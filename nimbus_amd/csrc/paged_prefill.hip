@@ -210,7 +210,8 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // keeps garbage out of O. K goes global -> LDS directly
   // (buffer_load_dwordx4 ... lds: lane l's 16 bytes land at the wave's LDS
   // base + 16 l), so each lane loads the chunk that the swizzle puts in its
-  // slot; V passes through registers for the fp16 conversion.
+  // slot. fp16 V goes the same way; bf16 V passes through registers for
+  // the fp16 conversion.
   const int32_t* btrow = a.bt + seq * a.bt_sb;
   const int last_page = (kv_end + 15) / 16 - 1;
   auto load_pages = [&](int blk) {
@@ -233,7 +234,8 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   for (int i = 0; i < PPT; ++i) {
     const int key = lkey + KSTEP * i;
     k_goff[i] = (key % 16) * row_bytes + 16 * k_pos<D>(key, lc);  // k_pos is an involution in the chunk index
-    v_goff[i] = (key % 16) * row_bytes + 16 * lc;
+    // (converting bf16 V in place in LDS instead measured slower)
+    v_goff[i] = (key % 16) * row_bytes + 16 * (DT == kFloat16 ? v_pos<D>(key, lc) : lc);  // v_pos is an involution too
     v_st[i] = key * D + 8 * v_pos<D>(key, lc);
   }
   // Buffer resource of the page holding piece i of this wave in block blk.
@@ -258,18 +260,29 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(page_rsrc(kbytes, p, blk, i), (lds_void*)dst, 16, k_goff[i], 0, 0, 0);
     }
   };
-  u32x4 vreg[PPT];
-  auto issue_v = [&](const BlockPages& p, int blk) {
-#pragma unroll
-    for (int i = 0; i < PPT; ++i) vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(page_rsrc(vbytes, p, blk, i), v_goff[i], 0, 0);
-  };
-  auto store_v = [&](auto slot) {
+  u32x4 vreg[DT == kFloat16 ? 1 : PPT];
+  // V(blk) into LDS slot `slot`: issued here, completed by store_v.
+  auto issue_v = [&](const BlockPages& p, int blk, auto slot) {
 #pragma unroll
     for (int i = 0; i < PPT; ++i) {
-      u32x4 v = vreg[i];
+      if constexpr (DT == kFloat16) {
+        uint16_t* dst = vs + slot * TILE + (wave * KPW + KSTEP * i) * D;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(page_rsrc(vbytes, p, blk, i), (lds_void*)dst, 16, v_goff[i], 0, 0,
+                                                 0);
+      } else {
+        vreg[i] = __builtin_amdgcn_raw_buffer_load_b128(page_rsrc(vbytes, p, blk, i), v_goff[i], 0, 0);
+      }
+    }
+  };
+  auto store_v = [&](auto slot) {
+    if constexpr (DT == kBFloat16) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = v_to_f16_pair<DT>(v[e]);
-      *reinterpret_cast<u32x4*>(vs + slot * TILE + v_st[i]) = v;
+      for (int i = 0; i < PPT; ++i) {
+        u32x4 v = vreg[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = v_to_f16_pair<DT>(v[e]);
+        *reinterpret_cast<u32x4*>(vs + slot * TILE + v_st[i]) = v;
+      }
     }
   };
 
@@ -400,7 +413,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   BlockPages pg_k = load_pages(kbeg + 2);  // pages of K(kb + 2)
   if (kend > kbeg) {
     const BlockPages pg0 = load_pages(kbeg);
-    issue_v(pg0, kbeg);
+    issue_v(pg0, kbeg, IntC<0>{});
     dma_k(pg0, kbeg, IntC<0>{});
     __syncthreads();
     dma_k(pg_v, kbeg + 1, IntC<1>{});  // past the context: zeros; past the piece: unused
@@ -421,7 +434,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     constexpr bool NEXT = decltype(has_next)::value;
     BlockPages pg_n;
     if constexpr (NEXT) {
-      issue_v(pg_v, kb + 1);
+      issue_v(pg_v, kb + 1, IntC<1 - SLOT>{});
       pg_n = load_pages(kb + 3);
       dma_k(pg_k, kb + 2, IntC<SLOT>{});
     }

@@ -36,11 +36,14 @@ def test_build_programs_matches_reference_loop(qs):
 @pytest.mark.parametrize("qs,ctx", [([0, 512, 1024, 1536, 2048], [700, 1536, 512, 1000]),
                                     ([0, 5, 69, 72], [5, 100, 3]), ([0, 64], [64]),
                                     ([0] + [512 * (i + 1) for i in range(6)], [2560] * 6),
-                                    ([0] + [200 * (i + 1) for i in range(12)], [300 + 50 * i for i in range(12)])])
+                                    ([0] + [200 * (i + 1) for i in range(12)], [300 + 50 * i for i in range(12)]),
+                                    ([0] + [300 * (i + 1) for i in range(8)], [400 + 90 * i for i in range(8)]),
+                                    ([0] + [600 * (i + 1) for i in range(8)], [900 + 90 * i for i in range(8)])])
 def test_build_programs_cost_order_keeps_the_entries(qs, ctx):
     """With context lengths the table holds the reference's entries: sequences
     heaviest first, each sequence's tiles adjacent and heaviest first, and,
-    for a table short enough to start at once, the second half reversed."""
+    for a table short enough to start at once, the second half reversed; a
+    table of up to LPT_TILES tiles goes heaviest tile first."""
     s, m = prefill_attention.build_programs(qs, "cpu", ctx)
     got = list(zip(s.tolist(), m.tolist()))
     entries = _programs_loop(qs)
@@ -51,6 +54,10 @@ def test_build_programs_cost_order_keeps_the_entries(qs, ctx):
     half = (len(got) + 1) // 2
     paired = len(got) <= prefill_attention.PAIRED_TILES
     listed = got[:half] + got[half:][::-1] if paired else got
+    if prefill_attention.PAIRED_TILES < len(got) <= prefill_attention.LPT_TILES:
+        keys = [(-cost[(a, b)], a, b) for a, b in listed]
+        assert keys == sorted(keys)
+        return
     keys = [(-seq_cost[a], a, -cost[(a, b)]) for a, b in listed]
     assert keys == sorted(keys)
     # each sequence's tiles stay together in the listed order
