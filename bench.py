@@ -24,6 +24,9 @@ cpu_baseline the CPU oracle (restated nimbus/kernels/reference.py:71-96,
 prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
              prefixes of up to 1024): causal FLOPs / mean time per call of K
              back-to-back calls, against the 2.5 PFLOP/s dense bf16 MFMA peak
+prefill_scaling the same prefill kernel on two larger workloads (not BASELINE
+             configs): one 8192-token prompt, and 64 chunks of 512 over
+             2048-token cached prefixes; at most 20 timed calls each
 mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
              (eager) + the 60 decodes replayed from a hipGraph padded to 64
 verify       speculative verification's attention (16 sequences x 5 tokens)
@@ -286,6 +289,27 @@ def time_prefill(batch, steps, warmup):
     flops = workloads.prefill_flops(seqs, h, d)
     return {"us_per_call": us, "us_per_call_event_pairs": us_pairs, "flops": flops, "tflops": flops / us / 1e6,
             "tiles": int(progs[0].numel())}
+
+
+def prefill_scaling(steps, warmup):
+    """The config-4 prefill kernel (Llama-3-8B heads, bf16) where the chip is
+    not bound by one unit's chain of key blocks: one 8192-token prompt, and
+    64 chunks of 512 on 2048-token cached prefixes."""
+    import torch
+
+    from nimbus_amd import workloads
+
+    rows = []
+    for label, seqs in (("one 8192-token prompt", [(8192, 8192)]),
+                        ("64 chunks of 512 on 2048-token prefixes", [(2048 + 512, 512)] * 64)):
+        b = workloads.build_batch(seqs, heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16, device="cuda",
+                                  seed=5)
+        r = time_prefill(b, steps, warmup)
+        rows.append({"workload": label, "us_per_call": r["us_per_call"], "flops": r["flops"],
+                     "tflops": r["tflops"], "frac_mfma_peak": r["tflops"] / MFMA_BF16_PEAK_TFLOPS})
+        del b
+        torch.cuda.empty_cache()
+    return rows
 
 
 def time_mixed_step(batch, steps, warmup):
@@ -722,6 +746,8 @@ def main(argv=None):
         result["mixed_step"] = time_mixed_step(mixed, args.steps, args.warmup)
         log(f"prefill: {result['prefill']}  mixed: {result['mixed_step']}")
         del mixed
+        result["prefill_scaling"] = prefill_scaling(min(args.steps, 20), min(args.warmup, 3))
+        log(f"prefill_scaling: {result['prefill_scaling']}")
     if not args.no_prefill:
         log("speculative verify")
         result["verify"] = time_verify(args.steps, args.warmup)
