@@ -470,11 +470,14 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
 // Second pass: for every sequence whose pages were split between waves,
 // o = sum_i O_i w_i / sum_i L_i w_i with w_i = 2^(m_i - max m) over its
 // pieces (nimbus/kernels/paged_attention.py:83-98). One workgroup per
-// (sequence, kv-head group), one lane per (column of the group, 8
-// consecutive elements of d); sequences held whole by one wave exit at once.
-// A long sequence has tens of pieces, so they are read kMergeBatch at a time,
-// every load of a batch issued before any is used: the pass costs a few
-// memory round trips instead of one per piece.
+// (sequence, kv-head group); sequences held whole by one wave exit at once.
+// A lane owns one column of the group and 8 consecutive elements of d; the
+// columns x D / 8 lanes this takes (64 for a decode kv head with G = 4) are
+// repeated over the workgroup's 256 lanes as piece groups, and group j
+// reads pieces i0 + j, i0 + j + groups, ..., kMergeBatch of them per round
+// trip, every load of a batch issued before any is used. So a sequence's
+// pieces (tens for a long context) arrive in one or two round trips; the
+// groups' running (M, L, O) are then combined through LDS by the same rule.
 constexpr int kMergeBatch = 8;
 constexpr int kMergeThreads = 256;  // 16 columns x D / 8 lanes (D <= 128)
 
@@ -482,6 +485,8 @@ template <int DT, int D>
 __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int SEG = D / 8;  // lanes per column
   static_assert(16 * SEG <= kMergeThreads, "one lane per (column, 8 elements of d)");
+  __shared__ float sm[kMergeThreads], sl[kMergeThreads];
+  __shared__ f32x4 so[2][kMergeThreads];
   const int b = blockIdx.x;
   const int kg = blockIdx.y;
   const int total = a.pre_out[a.B];
@@ -495,59 +500,79 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(Decod
   const int kvh = kg % a.nkv;
   const int g0 = (kg / a.nkv) * 16;
   const int gcount = min(16, a.nq * a.G - g0);
+  const int lanes = gcount * SEG;            // lanes of one piece group
+  const int groups = kMergeThreads / lanes;  // >= 1
   const int e = threadIdx.x;
-  if (e >= gcount * SEG) return;
-  const int vcol = g0 + e / SEG;
+  const int grp = e / lanes;
+  const int el = e - grp * lanes;
+  const int vcol = g0 + el / SEG;
   const int qj = vcol / a.G;
   const int head = kvh * a.G + vcol - qj * a.G;
   const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;
   const int64_t cols = static_cast<int64_t>(a.nq) * a.H;  // rows per slot
-  const int d0 = 8 * (e % SEG);
+  const int d0 = 8 * (el % SEG);
 
   float M = kNoScore, L = 0.f;
-  float O[8];
+  f32x4 O0 = f32x4{0.f, 0.f, 0.f, 0.f}, O1 = O0;
+  if (grp < groups) {
+    for (int i = i0 + grp; i <= i1; i += groups * kMergeBatch) {
+      float2 ml[kMergeBatch];
+      f32x4 o0[kMergeBatch], o1[kMergeBatch];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) O[k] = 0.f;
-  for (int i = i0; i <= i1; i += kMergeBatch) {
-    float2 ml[kMergeBatch];
-    f32x4 o0[kMergeBatch], o1[kMergeBatch];
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int64_t row = (static_cast<int64_t>(min(i + u * groups, i1)) + b) * cols + vhead;
+        ml[u] = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+        o0[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
+        o1[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
+      }
+      float mx = M;
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-      const int64_t row = (static_cast<int64_t>(min(i + u, i1)) + b) * cols + vhead;
-      ml[u] = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
-      o0[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
-      o1[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
-    }
-    float mx = M;
+      for (int u = 0; u < kMergeBatch; ++u) {
+        if (i + u * groups <= i1) mx = fmaxf(mx, ml[u].x);
+      }
+      const float wo = fast_exp2(M - mx);
+      L *= wo;
+      O0 *= wo;
+      O1 *= wo;
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-      if (i + u <= i1) mx = fmaxf(mx, ml[u].x);
-    }
-    const float wo = fast_exp2(M - mx);
-    L *= wo;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) O[k] *= wo;
-#pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-      if (i + u <= i1) {
-        const float wi = fast_exp2(ml[u].x - mx);
-        L += ml[u].y * wi;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          O[k] += o0[u][k] * wi;
-          O[k + 4] += o1[u][k] * wi;
+      for (int u = 0; u < kMergeBatch; ++u) {
+        if (i + u * groups <= i1) {
+          const float wi = fast_exp2(ml[u].x - mx);
+          L += ml[u].y * wi;
+          O0 += o0[u] * wi;
+          O1 += o1[u] * wi;
         }
       }
+      M = mx;
     }
-    M = mx;
+  }
+  // Groups without pieces keep M = kNoScore, L = 0, O = 0 and weigh nothing
+  // (group 0 always holds piece i0).
+  sm[e] = M;
+  sl[e] = L;
+  so[0][e] = O0;
+  so[1][e] = O1;
+  __syncthreads();
+  if (grp != 0) return;
+  for (int g = 1; g < groups; ++g) M = fmaxf(M, sm[g * lanes + el]);
+  const float w0 = fast_exp2(sm[el] - M);
+  L *= w0;
+  O0 *= w0;
+  O1 *= w0;
+  for (int g = 1; g < groups; ++g) {
+    const int j = g * lanes + el;
+    const float w = fast_exp2(sm[j] - M);
+    L += sl[j] * w;
+    O0 += so[0][j] * w;
+    O1 += so[1][j] * w;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   const int64_t tok = static_cast<int64_t>(b) * a.nq + qj;
   uint16_t* orow = a.out + tok * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
-  const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O[0] * inv), Elem<DT>::from_f32(O[1] * inv)),
-                        pack2(Elem<DT>::from_f32(O[2] * inv), Elem<DT>::from_f32(O[3] * inv)),
-                        pack2(Elem<DT>::from_f32(O[4] * inv), Elem<DT>::from_f32(O[5] * inv)),
-                        pack2(Elem<DT>::from_f32(O[6] * inv), Elem<DT>::from_f32(O[7] * inv))};
+  const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O0[0] * inv), Elem<DT>::from_f32(O0[1] * inv)),
+                        pack2(Elem<DT>::from_f32(O0[2] * inv), Elem<DT>::from_f32(O0[3] * inv)),
+                        pack2(Elem<DT>::from_f32(O1[0] * inv), Elem<DT>::from_f32(O1[1] * inv)),
+                        pack2(Elem<DT>::from_f32(O1[2] * inv), Elem<DT>::from_f32(O1[3] * inv))};
   *reinterpret_cast<u32x4*>(orow) = w;
 }
 
