@@ -28,7 +28,9 @@ prefill_scaling the same prefill kernel on two larger workloads (not BASELINE
              configs): one 8192-token prompt, and 64 chunks of 512 over
              2048-token cached prefixes; at most 20 timed calls each
 mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
-             (eager) + the 60 decodes replayed from a hipGraph padded to 64
+             (eager) + the 60 decodes replayed from a hipGraph padded to 64;
+             `write_kv` is the slot write of all 2,108 tokens alone (k and v
+             rows read and written + slots, against 8 TB/s)
 verify       speculative verification's attention (16 sequences x 5 tokens)
              replayed from a hipGraph, with the decode kernel on the same
              contexts beside it
@@ -287,8 +289,9 @@ def time_prefill(batch, steps, warmup):
     seqs = batch.seqs[:batch.num_prefills]
     h, d = batch.q.shape[1], batch.q.shape[2]
     flops = workloads.prefill_flops(seqs, h, d)
+    nbytes = workloads.prefill_bytes(seqs, h, batch.k_cache.shape[2], d, batch.q.element_size())
     return {"us_per_call": us, "us_per_call_event_pairs": us_pairs, "flops": flops, "tflops": flops / us / 1e6,
-            "tiles": int(progs[0].numel())}
+            "bytes": nbytes, "tiles": int(progs[0].numel())}
 
 
 def prefill_scaling(steps, warmup):
@@ -316,6 +319,7 @@ def time_mixed_step(batch, steps, warmup):
     """write_kv for every token + prefill (eager) + decode via hipGraph at padded 64."""
     import torch
 
+    from nimbus_amd import workloads
     from nimbus_amd.graphs import DecodeAttentionGraphs
     from nimbus_amd.kernels.cache_ops import write_kv
     from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
@@ -343,8 +347,19 @@ def time_mixed_step(batch, steps, warmup):
         step(i)
     us = event_times_us(step, steps, torch.cuda.current_stream())
     replay_us = event_times_us(lambda i: graphs.replay(gb), steps, torch.cuda.current_stream())
+    # The slot write alone (all 2,108 tokens of the step), 32 calls back to back in a hipGraph (eager calls
+    # would time the host wrapper): algorithmic bytes = k and v rows read and written + the int64 slots.
+    def write_all():
+        write_kv(batch.k, batch.v, kc, vc, batch.slot_mapping)
+
+    with torch.inference_mode():  # as the decode graphs were captured (their generator state is an inference tensor)
+        w_us = _graph_us([write_all] * 32, steps, warmup)
+    kvh, d = batch.k.shape[1], batch.k.shape[2]
+    w_bytes = workloads.write_kv_bytes(int(batch.k.shape[0]), kvh, d, batch.k.element_size())
     return {"step_us": statistics.mean(us), "decode_graph_replay_us": statistics.mean(replay_us),
-            "padded_batch": gb, "tokens": int(batch.q.shape[0])}
+            "padded_batch": gb, "tokens": int(batch.q.shape[0]),
+            "write_kv": {"us_per_call": w_us, "bytes": w_bytes, "GBps": w_bytes / w_us / 1e3,
+                         "frac_hbm_peak": w_bytes / w_us / 1e3 / HBM_PEAK_GBS}}
 
 
 # ---------------------------------------------------------------- speculative verification

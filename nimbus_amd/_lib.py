@@ -135,5 +135,3 @@ def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
-def ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
