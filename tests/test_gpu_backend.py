@@ -158,3 +158,44 @@ def test_verify_graph_replay_matches_eager_and_oracle(n, q_len, dtype):
     assert torch.equal(kc[:nb], kc_e[:nb]) and torch.equal(vc[:nb], vc_e[:nb])
     want = oracle_prefill(b.q, kc_e, vc_e, pa[7], pa[8], b.block_tables, b.scale)
     assert_within(replays[0].cpu(), want, what="verify replay vs oracle")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_mixed_batches_match_oracle(seed):
+    """Seeded random flat batches through the backend, as runner.prepare lays
+    them out: a few prefill chunks (fresh prompts and chunks over cached
+    prefixes, lengths crossing tile and page edges) then decodes, over
+    random head shapes, head dims and dtypes. The slot write is bit-exact and
+    both parts match the oracle."""
+    import numpy as np
+
+    rng = np.random.default_rng(100 + seed)
+    heads, kv = [(32, 8), (32, 4), (16, 16), (28, 4), (32, 1)][int(rng.integers(0, 5))]
+    d = int(rng.choice([64, 128]))
+    dtype = [torch.float16, torch.bfloat16][seed % 2]
+    seqs = []
+    for _ in range(int(rng.integers(1, 5))):
+        q_len = int(rng.integers(1, 700))
+        prefix = int(rng.choice([0, int(rng.integers(1, 1500))]))
+        seqs.append((prefix + q_len, q_len))
+    seqs = [s for s in seqs if s[1] > 1 or s[0] == 1] or [(65, 65)]
+    seqs += [(int(rng.integers(1, 3000)), 1) for _ in range(int(rng.integers(0, 40)))]
+    announce(f"backend random batch seed={seed} H={heads} KV={kv} D={d} {dtype} prefills={sum(q > 1 for _, q in seqs)} "
+             f"decodes={sum(q == 1 for _, q in seqs)}")
+    b = workloads.build_batch(seqs, heads=heads, kv_heads=kv, head_dim=d, dtype=dtype, device="cuda", seed=seed,
+                              write_first=False)
+    k_before = b.k_cache.clone()
+    out = AttentionBackend().forward(b.q, b.k, b.v, b.k_cache, b.v_cache, _meta(b), b.scale)
+    torch.cuda.synchronize()
+    kref = k_before.view(-1, kv, d)
+    kref[b.slot_mapping] = b.k
+    assert torch.equal(b.k_cache.view(-1, kv, d).view(torch.int16), kref.view(torch.int16))
+    p = b.num_prefill_tokens
+    if p:
+        q, k, v, _, _, bt, scale, qs, ctx = b.prefill_args()
+        assert_within(out[:p].cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="prefill part")
+    if b.num_prefills < len(seqs):
+        da = b.decode_args()
+        assert_within(out[p:].cpu(),
+                      oracle_decode(da[0], b.k_cache, b.v_cache, b.decode_context_host(), da[4], b.scale),
+                      what="decode part")
