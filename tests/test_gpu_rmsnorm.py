@@ -48,7 +48,7 @@ def _inputs(rows, cols, dtype, seed, scale=1.0):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("rows,cols", [(1, 2048), (37, 2048), (5, 768), (3, 4096), (2048, 2048), (64, 4096),
-                                       (7, 8192), (513, 8), (9, 520)])
+                                       (7, 8192), (513, 8), (9, 520), (2109, 4096), (2049, 768), (4100, 2048)])
 def test_add_rms_norm_matches_oracle(dtype, rows, cols):
     announce(f"add_rms_norm dtype={dtype} rows={rows} cols={cols}")
     x, r, w = _inputs(rows, cols, dtype, rows * 7 + cols)
@@ -60,7 +60,7 @@ def test_add_rms_norm_matches_oracle(dtype, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("rows,cols", [(1, 2048), (37, 2048), (5, 768), (3, 4096)])
+@pytest.mark.parametrize("rows,cols", [(1, 2048), (37, 2048), (5, 768), (3, 4096), (2051, 2048)])
 def test_rms_norm_matches_oracle(dtype, rows, cols):
     announce(f"rms_norm dtype={dtype} rows={rows} cols={cols}")
     x, _, w = _inputs(rows, cols, dtype, rows + cols)
