@@ -11,16 +11,25 @@ A step is one paged_decode_attention call on inputs already resident in HBM.
 value        algorithmic bytes of one call / wall time per step (GB/s):
              every visible K and V row once, q and out once, the page ids and
              context lengths (nimbus_amd.workloads.decode_bytes)
-roofline     the page pass (paged_decode_kernel, the dominant kernel) alone,
-             K launches back to back between one HIP event pair on the launch
-             stream: algorithmic bytes / mean duration per launch, against
-             8 TB/s (`kernel_us_event_pairs`: the mean with an event pair
-             around each launch, which adds its dispatch latency); `traffic` is the HBM bytes
-             per launch that rocprofv3 FETCH_SIZE + WRITE_SIZE measured for
-             this kernel and workload (profiles/decode_llama3_traffic.json,
-             scaled by the plain-copy calibration), null when absent
+roofline     the whole decode call (paged_decode_kernel, the page pass, then
+             paged_decode_merge_kernel, the split merge), K calls back to back
+             between one HIP event pair on the launch stream: algorithmic
+             bytes / mean time per call, against 8 TB/s
+             (`kernel_us_event_pairs`: the mean with an event pair around
+             each call, which adds its dispatch latency); `page_pass` gives
+             the page pass alone the same way; `traffic` is the HBM bytes per
+             call (both kernels) that rocprofv3 FETCH_SIZE + WRITE_SIZE
+             counted on this workload (profiles/decode_llama3_traffic.json,
+             scaled by the plain-copy calibration), null when absent or
+             measured on other decode sources (a sha256 of them is kept)
 cpu_baseline the CPU oracle (restated nimbus/kernels/reference.py:71-96,
-             batched exact form) on this host's cores, same inputs
+             batched exact form) on this host's cores, same inputs; `entries`
+             adds config 4's prefill part through the prefill oracle
+             (reference.py:37-68) and config 5 through the per-row decode
+             form, each a bounded sample
+reference_shapes the reference's own kernel micro-bench shapes
+             (bench/kernels.py:54-74: TinyLlama heads, fp16) beside its
+             published numbers (other hardware)
 prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
              prefixes of up to 1024): causal FLOPs / mean time per call of K
              back-to-back calls, against the 2.5 PFLOP/s dense bf16 MFMA peak
@@ -106,17 +115,35 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def measured_traffic(kernel, algorithmic_bytes):
-    """HBM bytes per launch of `kernel` on this workload as rocprofv3 counted
-    them (FETCH_SIZE + WRITE_SIZE, calibrated), from the committed profile
-    summary; None when there is none for this kernel and byte count."""
-    path = os.path.join(ROOT, "profiles", "decode_llama3_traffic.json")
+TRAFFIC_RECORD = os.path.join(ROOT, "profiles", "decode_llama3_traffic.json")
+DECODE_SOURCES = ("nimbus_amd/csrc/paged_decode.hip", "nimbus_amd/csrc/common.h",
+                  "nimbus_amd/csrc/nimbus_attn_internal.h", "include/nimbus_attn.h")
+
+
+def decode_source_hash():
+    """sha256 over the sources the decode kernels are compiled from, so a
+    traffic record measured on other code is recognised as stale."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for rel in DECODE_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(rel.encode() + b"\0" + f.read())
+    return h.hexdigest()
+
+
+def measured_traffic(algorithmic_bytes):
+    """HBM bytes of one decode call (page pass + merge pass) on this workload
+    as rocprofv3 counted them (FETCH_SIZE + WRITE_SIZE per dispatch, scaled
+    by the plain-copy calibration), from the committed record; None when the
+    record is absent, was measured on another workload, or on other decode
+    sources than the ones built here."""
     try:
-        with open(path) as f:
+        with open(TRAFFIC_RECORD) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None
-    if rec.get("kernel") != kernel or rec.get("algorithmic_bytes") != algorithmic_bytes:
+    if rec.get("algorithmic_bytes") != algorithmic_bytes or rec.get("source_sha256") != decode_source_hash():
         return None
     return rec.get("traffic_bytes")
 
@@ -216,10 +243,38 @@ def time_decode(batch, steps, warmup, wall=True):
     return res
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def _timed_reps(fn, seconds, reps=3):
+    """One warm-up call, then up to `reps` timed calls within `seconds`;
+    returns (median seconds, timed reps)."""
+    t = time.perf_counter()
+    fn()
+    first = time.perf_counter() - t
+    times = []
+    budget = time.perf_counter() + seconds
+    while len(times) < reps and time.perf_counter() + first < budget:
+        t = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t)
+    if not times:
+        times = [first]
+    return statistics.median(times), len(times)
+
+
 def cpu_decode_baseline(batch, seconds):
     """The CPU oracle (batched exact form of nimbus/kernels/reference.py:71-96)
-    on CPU copies of the same inputs: one warm-up, then up to 3 timed reps
-    within `seconds`."""
+    on CPU copies of the same inputs, in their dtype: one warm-up, then up to
+    3 timed reps within `seconds`."""
     import torch
 
     from nimbus_amd import workloads
@@ -234,36 +289,85 @@ def cpu_decode_baseline(batch, seconds):
     bt = batch.block_tables[p:].cpu()
     maxc = max(ctx_lens)
     h, d, kv = q.shape[1], q.shape[2], kc.shape[2]
-    t = time.perf_counter()
-    reference.paged_decode_attention(q, kc, vc, ctx, bt, maxc, batch.scale)
-    first = time.perf_counter() - t
-    times = []
-    budget = time.perf_counter() + seconds
-    while len(times) < 3 and time.perf_counter() + first < budget:
-        t = time.perf_counter()
-        reference.paged_decode_attention(q, kc, vc, ctx, bt, maxc, batch.scale)
-        times.append(time.perf_counter() - t)
-    if not times:
-        times = [first]
-    med = statistics.median(times)
+    med, n = _timed_reps(lambda: reference.paged_decode_attention(q, kc, vc, ctx, bt, maxc, batch.scale), seconds)
     nbytes = workloads.decode_bytes(ctx_lens, h, kv, d, q.element_size())
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {
         "value": nbytes / med / 1e9,
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"full llama3_decode batch (B={len(ctx_lens)}, sum ctx {sum(ctx_lens)}) through the batched "
-                   f"CPU oracle, median of {len(times)} reps after 1 warm-up: {med * 1e3:.1f} ms/call; "
-                   f"host {cpu_model}, os.cpu_count()={os.cpu_count()}"),
+        "sample": (f"config 3: the whole llama3_decode batch (B={len(ctx_lens)}, sum ctx {sum(ctx_lens)}) through the "
+                   f"batched CPU oracle, median of {n} reps after 1 warm-up: {med * 1e3:.1f} ms/call; "
+                   f"host {_cpu_model()}, os.cpu_count()={os.cpu_count()}"),
+    }
+
+
+def cpu_prefill_baseline(batch, seconds):
+    """The CPU oracle of paged prefill (nimbus/kernels/reference.py:37-68) on
+    CPU copies of BASELINE config 4's prefill part, in their dtype."""
+    import torch
+
+    from nimbus_amd import workloads
+    from oracle import reference
+
+    pa = batch.prefill_args()
+    q, kc, vc = pa[0].cpu(), batch.k_cache.cpu(), batch.v_cache.cpu()
+    qs, ctx, bt = pa[3].cpu(), pa[4].cpu(), pa[5].cpu()
+    med, n = _timed_reps(lambda: reference.paged_prefill_attention(q, kc, vc, qs, ctx, bt, batch.scale, pa[7], pa[8]),
+                         seconds)
+    seqs = batch.seqs[:batch.num_prefills]
+    flops = workloads.prefill_flops(seqs, q.shape[1], q.shape[2])
+    return {
+        "value": flops / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config 4's prefill part (4 chunks of 512 on prefixes {[c - ql for c, ql in seqs]}, "
+                   f"{flops / 1e9:.2f} GFLOP causal) through the CPU oracle, median of {n} reps after 1 warm-up: "
+                   f"{med * 1e3:.1f} ms/call"),
+    }
+
+
+def cpu_long_decode_baseline(batch, seconds):
+    """The per-row form of the decode oracle (oracle/reference.py's
+    decode_attention_rows: the math of nimbus/kernels/reference.py:71-96 one
+    sequence at a time; the batched form would gather a [256, 32768, 8, 128]
+    tensor) on BASELINE config 5, row by row in batch order until `seconds`
+    of oracle time are spent: bytes of the rows done / their oracle time.
+    Each row's pages are copied to the host before its timed call."""
+    import torch
+
+    from nimbus_amd import workloads
+    from oracle import reference
+
+    p = batch.num_prefills
+    t0 = batch.num_prefill_tokens
+    ctx_lens = batch.decode_context_host()
+    q_all = batch.q[t0:]
+    bt = batch.block_tables[p:]
+    h, d, kv = q_all.shape[1], q_all.shape[2], batch.k_cache.shape[2]
+    spent, done = 0.0, []
+    for b, c in enumerate(ctx_lens):
+        n = -(-c // 16)
+        pages = bt[b, :n].long()
+        kc, vc = batch.k_cache[pages].cpu(), batch.v_cache[pages].cpu()
+        q = q_all[b:b + 1].cpu()
+        table = torch.arange(n, dtype=torch.int32)[None]
+        t = time.perf_counter()
+        reference.decode_attention_rows(q, kc, vc, [c], table, batch.scale)
+        spent += time.perf_counter() - t
+        done.append(c)
+        if spent >= seconds:
+            break
+    nbytes = workloads.decode_bytes(done, h, kv, d, q_all.element_size())
+    return {
+        "value": nbytes / spent / 1e9,
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"config 5, per-row form: the first {len(done)} of {len(ctx_lens)} rows in batch order "
+                   f"(sum ctx {sum(done)} of {sum(ctx_lens)}), one oracle call per row, "
+                   f"{spent:.1f} s of oracle time"),
     }
 
 
@@ -559,8 +663,8 @@ def time_decode_step(steps, warmup, chain=16):
     from nimbus_amd.graphs import DecodeGraphs
     from nimbus_amd.model.config import LLAMA3_8B as cfg
     from nimbus_amd.model.llama import build_model
-    from nimbus_amd.model.runner import Sequence, prepare
     from nimbus_amd.quant import quantize_model, weight_bytes
+    from nimbus_amd.workloads import SeqState, flat_step
 
     bs = 16
     ctx = workloads.llama3_decode_lens(seed=0, batch=64)
@@ -574,11 +678,9 @@ def time_decode_step(steps, warmup, chain=16):
     caches = [(torch.randn(shape, generator=g, device="cuda").mul_(0.5).bfloat16(),
                torch.randn(shape, generator=g, device="cuda").mul_(0.5).bfloat16()) for _ in range(cfg.num_layers)]
     seqs = []
-    for i, c in enumerate(ctx):
-        s = Sequence(i, [rng.randrange(cfg.vocab_size) for _ in range(c)])
-        s.num_computed = c - 1
-        s.block_table = [pool.pop() for _ in range(-(-(c + 2 * chain + 8) // bs))]
-        seqs.append(s)
+    for c in ctx:
+        seqs.append(SeqState([rng.randrange(cfg.vocab_size) for _ in range(c)],
+                             [pool.pop() for _ in range(-(-(c + 2 * chain + 8) // bs))], c - 1))
     kv_bytes = sum(ctx) * cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
 
     def measure(label):
@@ -587,13 +689,13 @@ def time_decode_step(steps, warmup, chain=16):
         graphs.capture()
         batch = [(s, 1) for s in seqs]
         for _ in range(warmup):
-            st = prepare(batch, bs, "cuda")
+            st = flat_step(batch, "cuda", bs)
             model.logits(model(st.input_ids, st.positions, caches, st.meta))
         torch.cuda.synchronize()
         n = max(3, steps // 10)
         t0 = time.perf_counter()
         for _ in range(n):
-            st = prepare(batch, bs, "cuda")
+            st = flat_step(batch, "cuda", bs)
             model.logits(model(st.input_ids, st.positions, caches, st.meta))
         torch.cuda.synchronize()
         eager_ms = (time.perf_counter() - t0) * 1e3 / n
@@ -620,6 +722,68 @@ def time_decode_step(steps, warmup, chain=16):
     del model, caches
     torch.cuda.empty_cache()
     return res
+
+
+# ---------------------------------------------------------------- the reference's own micro-bench shapes
+
+# Published on an RTX 4050 Laptop GPU (results/kernels.json:15-71 of the reference, triton_us), for the table's
+# other column; not a target (other hardware).
+REFERENCE_PUBLISHED_US = {
+    "paged_decode_attention batch=1 ctx=512": 26.2, "paged_decode_attention batch=1 ctx=2048": 39.9,
+    "paged_decode_attention batch=16 ctx=512": 98.3, "paged_decode_attention batch=64 ctx=512": 348.3,
+    "paged_decode_attention batch=64 ctx=1024": 626.7, "paged_prefill_attention seqs=1 len=512": 118.9,
+    "paged_prefill_attention seqs=4 len=512": 383.4, "paged_prefill_attention seqs=16 len=128": 203.4,
+}
+
+
+def reference_shapes(reps=200, warmup=25):
+    """The shapes of the reference's kernel micro-bench (bench/kernels.py:54-74):
+    TinyLlama heads (H=32, KV=4, D=64), fp16, pages a seeded permutation of
+    a pool of (pages needed + 8) blocks; decode at (batch, ctx) in {(1,512),
+    (1,2048), (16,512), (64,512), (64,1024)}, fresh prefill of (seqs, len) in
+    {(1,512), (4,512), (16,128)}. Each call is timed alone between a HIP event
+    pair through the Python entry point (as triton.testing.do_bench does),
+    median of `reps`. The pools are at most 17 MB, so they sit in the Infinity
+    Cache: GB/s here is effective, not HBM."""
+    import torch
+
+    from nimbus_amd import workloads
+    from nimbus_amd.kernels.paged_attention import paged_decode_attention
+    from nimbus_amd.kernels.prefill_attention import paged_prefill_attention
+
+    rows = []
+    stream = torch.cuda.current_stream()
+    for b, ctx in ((1, 512), (1, 2048), (16, 512), (64, 512), (64, 1024)):
+        batch = workloads.build_batch([(ctx, 1)] * b, heads=32, kv_heads=4, head_dim=64, dtype=torch.float16,
+                                      device="cuda", seed=0, pool_blocks=b * -(-ctx // 16) + 8,
+                                      contiguous_slices=True, write_first=False)
+        a = batch.decode_args()
+        out = torch.empty_like(a[0])
+        fn = lambda i: paged_decode_attention(*a, out=out)  # noqa: E731
+        for i in range(warmup):
+            fn(i)
+        us = statistics.median(event_times_us(fn, reps, stream))
+        nbytes = workloads.decode_bytes([ctx] * b, 32, 4, 64, 2)
+        name = f"paged_decode_attention batch={b} ctx={ctx}"
+        rows.append({"kernel": name, "us": us, "GBps_effective": nbytes / us / 1e3,
+                     "reference_published_us": REFERENCE_PUBLISHED_US[name]})
+    for n, ql in ((1, 512), (4, 512), (16, 128)):
+        batch = workloads.build_batch([(ql, ql)] * n, heads=32, kv_heads=4, head_dim=64, dtype=torch.float16,
+                                      device="cuda", seed=0, pool_blocks=n * -(-ql // 16) + 8,
+                                      contiguous_slices=True)
+        a = batch.prefill_args()
+        out = torch.empty_like(a[0])
+        fn = lambda i: paged_prefill_attention(*a, out=out)  # noqa: E731
+        for i in range(warmup):
+            fn(i)
+        us = statistics.median(event_times_us(fn, reps, stream))
+        flops = workloads.prefill_flops([(ql, ql)] * n, 32, 64)
+        name = f"paged_prefill_attention seqs={n} len={ql}"
+        rows.append({"kernel": name, "us": us, "TFLOPs": flops / us / 1e6,
+                     "frac_mfma_peak": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS,
+                     "reference_published_us": REFERENCE_PUBLISHED_US[name]})
+    return {"note": "reference_published_us: the reference's Triton kernels on an RTX 4050 Laptop GPU "
+                    "(results/kernels.json), other hardware", "rows": rows}
 
 
 # ---------------------------------------------------------------- configs 1, 2 and 5
@@ -717,6 +881,7 @@ def main(argv=None):
     batch = workloads.llama3_decode("cuda")
     dec = time_decode(batch, args.steps, args.warmup)
     log(f"decode: {dec}")
+    call_gbs = dec["bytes"] / dec["call_us"] / 1e3
     part_gbs = dec["bytes"] / dec["page_pass_us"] / 1e3
     result = {
         "metric": METRIC,
@@ -739,15 +904,18 @@ def main(argv=None):
         },
         "us_per_call": dec["call_us"],
         "roofline": {
-            "kernel": "paged_decode_kernel (page pass)",
+            "kernel": "paged_decode_kernel + paged_decode_merge_kernel (the whole decode call)",
             "bound": "hbm",
-            "achieved": part_gbs,
+            "achieved": call_gbs,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": part_gbs / HBM_PEAK_GBS,
-            "traffic": measured_traffic("paged_decode_kernel", dec["bytes"]),
-            "kernel_us": dec["page_pass_us"],
-            "kernel_us_event_pairs": dec["page_pass_us_event_pairs"],
+            "frac": call_gbs / HBM_PEAK_GBS,
+            "traffic": measured_traffic(dec["bytes"]),
+            "kernel_us": dec["call_us"],
+            "kernel_us_event_pairs": dec["call_us_event_pairs"],
+            "page_pass": {"kernel": "paged_decode_kernel", "us": dec["page_pass_us"],
+                          "us_event_pairs": dec["page_pass_us_event_pairs"], "achieved": part_gbs,
+                          "frac": part_gbs / HBM_PEAK_GBS},
             "merge_pass_share_us": dec["merge_us"],
         },
     }
@@ -778,12 +946,28 @@ def main(argv=None):
         log(f"decode_step: {result['decode_step']}")
     if not args.no_prefill:
         result["other_configs"] = other_configs(min(args.steps, 50), args.warmup)
+        log("reference_shapes")
+        result["reference_shapes"] = reference_shapes()
+        log(f"reference_shapes: {result['reference_shapes']}")
     if args.all:
         result["configs"] = {k: {a: b for a, b in v.items() if not isinstance(b, dict)}
                              for k, v in all_configs(args.steps, args.warmup).items()}
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle on host cores)")
-        result["cpu_baseline"] = cpu_decode_baseline(batch, args.cpu_seconds)
+        base = cpu_decode_baseline(batch, args.cpu_seconds)
+        entries = [dict(base, config="config 3 (headline), batched form")]
+        del batch
+        torch.cuda.empty_cache()
+        if not args.no_prefill:
+            mixed = workloads.llama3_mixed("cuda")
+            entries.append(dict(cpu_prefill_baseline(mixed, args.cpu_seconds), config="config 4 prefill part"))
+            del mixed
+            torch.cuda.empty_cache()
+            long_b = workloads.llama3_long_decode("cuda")
+            entries.append(dict(cpu_long_decode_baseline(long_b, args.cpu_seconds), config="config 5, per-row form"))
+            del long_b
+            torch.cuda.empty_cache()
+        result["cpu_baseline"] = dict(base, entries=entries)
     print(json.dumps(result), flush=True)
 
 

@@ -17,6 +17,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -50,19 +51,30 @@ def flags() -> list[str]:
     ]
 
 
-def build(verbose: bool = False) -> str:
-    """Compiles every source into LIB_PATH (always recompiles). Returns the path."""
-    cc = hipcc()
-    tmp = LIB_PATH + ".tmp"
-    cmd = [cc, *flags(), "-shared", "-o", tmp, *[os.path.join(CSRC, s) for s in SOURCES]]
-    if verbose:
-        cmd.insert(1, "-Rpass-analysis=kernel-resource-usage")
+def _run(cmd: list[str], verbose: bool) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed ({res.returncode}): {' '.join(cmd)}")
     if verbose:
         sys.stdout.write(res.stderr)
+
+
+def build(verbose: bool = False, jobs: int | None = None) -> str:
+    """Compiles every source into LIB_PATH (always recompiles): one object per
+    source, compiled in parallel, then one link. Returns the path."""
+    cc = hipcc()
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    extra = ["-Rpass-analysis=kernel-resource-usage"] if verbose else []
+    objs = [os.path.join(objdir, os.path.splitext(s)[0] + ".o") for s in SOURCES]
+    cmds = [[cc, *extra, *flags(), "-c", "-o", o, os.path.join(CSRC, s)] for s, o in zip(SOURCES, objs)]
+    workers = jobs or min(len(cmds), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for fut in [pool.submit(_run, c, verbose) for c in cmds]:
+            fut.result()
+    tmp = LIB_PATH + ".tmp"
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose=False)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

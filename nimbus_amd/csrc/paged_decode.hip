@@ -53,6 +53,8 @@
 // The grid depends only on host integers (batch, kv heads, max_context and
 // the device's CU count), so a call is capturable in a hipGraph, and no
 // workgroup is launched beyond what the chip holds at once.
+#include <atomic>
+
 #include "common.h"
 #include "nimbus_attn_internal.h"
 
@@ -594,12 +596,24 @@ static int64_t waves_per_group(int64_t cus, int kvg, int64_t max_pages) {
   return n < 1 ? 1 : n;
 }
 
+// CU count of the current device, asked of the runtime once per device and
+// kept (a device's CU count does not change while the process runs).
+constexpr int kMaxDevices = 64;
+static std::atomic<int> g_device_cus[kMaxDevices];  // 0: not asked yet
+
 static int device_cus(int64_t* cus) {
-  int dev = 0, n = 0;
+  int dev = 0;
   hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  const bool slot = dev >= 0 && dev < kMaxDevices;
+  int n = slot ? g_device_cus[dev].load(std::memory_order_relaxed) : 0;
+  if (n <= 0) {
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (slot) g_device_cus[dev].store(n, std::memory_order_relaxed);
+  }
   *cus = n;
-  return static_cast<int>(e);
+  return 0;
 }
 
 // phase bit 1: page pass, bit 2: merge pass.

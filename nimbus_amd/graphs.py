@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import bisect
 
+import numpy as np
 import torch
 
 from nimbus_amd.kernels.elementwise import greedy_step
@@ -41,6 +42,7 @@ from nimbus_amd.kernels.paged_attention import (PAGE, decode_workspace_bytes, ne
                                                 verify_workspace_bytes)
 from nimbus_amd.kernels.prefill_attention import verify_queries
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
+from nimbus_amd.workloads import is_decode
 
 PADDED_SIZES = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128)
 
@@ -353,9 +355,9 @@ class DecodeGraphs:
         torch.cuda.synchronize()
 
     def can_run(self, batch) -> bool:
-        """(sequence, tokens) pairs that are all plain decodes (cuda_graph.py:83-85)."""
-        return 0 < len(batch) <= self.max_batch and all(
-            n == 1 and s.num_computed > 0 and s.num_computed + 1 == len(s) for s, n in batch)
+        """True for (sequence, tokens) pairs that are all plain decodes and fit
+        the captured sizes (the condition of cuda_graph.py:83-85)."""
+        return 0 < len(batch) <= self.max_batch and all(is_decode(s, n) for s, n in batch)
 
     @torch.inference_mode()
     def run(self, seqs) -> torch.Tensor:
@@ -380,35 +382,38 @@ class DecodeGraphs:
         return self.tokens[:n, :steps].clone()
 
     def _load(self, seqs) -> int:
-        """Copies seqs' next-token inputs into the static buffers (through
-        pinned staging, cuda_graph.py:118-144); returns the captured size."""
+        """Stages seqs' next-token inputs into the static buffers and pads the
+        batch to a captured size (the contract of cuda_graph.py:118-144):
+        each real row feeds token num_computed at that position, writing slot
+        table[p // bs] * bs + p % bs, with context p + 1; padding rows feed
+        token 0 at position 0 with context 1 on the scratch block. The rows
+        are assembled in pinned host memory and copied in one go per buffer.
+        Returns the captured size."""
         n = len(seqs)
         if not 0 < n <= self.max_batch:
             raise ValueError(f"batch {n} outside 1..{self.max_batch}")
         b = self.sizes[bisect.bisect_left(self.sizes, n)]
         bs = self.block_size
-        h, ht = self._host, self._host_tables
         if self._staged is not None:
             self._staged.synchronize()  # the previous call's copies have read the pinned rows
+        rows, tables = self._host.numpy(), self._host_tables.numpy()
+        widths = [len(s.block_table) for s in seqs]
+        if max(widths) > tables.shape[1]:
+            raise ValueError("a block table is wider than max_model_len allows")
+        tables[:n] = 0
         for i, s in enumerate(seqs):
-            p = s.num_computed
-            if len(s.block_table) > ht.shape[1]:
-                raise ValueError("a block table is wider than max_model_len allows")
-            h[0, i] = s.token_ids[p]
-            h[1, i] = p
-            h[2, i] = s.block_table[p // bs] * bs + p % bs
-            h[3, i] = p + 1
-            ht[i, :len(s.block_table)] = torch.as_tensor(s.block_table, dtype=torch.int32)
-        h[0, n:b] = 0
-        h[1, n:b] = 0
-        h[2, n:b] = self.scratch_slot
-        h[3, n:b] = 1
-        ht[n:b, 0] = self.scratch_block
-        self.input_ids[:b].copy_(h[0, :b], non_blocking=True)
-        self.positions[:b].copy_(h[1, :b], non_blocking=True)
-        self.slots[:b].copy_(h[2, :b], non_blocking=True)
-        self.ctx[:b].copy_(h[3, :b], non_blocking=True)
-        self.tables[:b].copy_(ht[:b], non_blocking=True)
+            tables[i, :widths[i]] = s.block_table
+        pos = np.fromiter((s.num_computed for s in seqs), dtype=np.int64, count=n)
+        rows[0, :n] = [s.token_ids[p] for s, p in zip(seqs, pos.tolist())]
+        rows[1, :n] = pos
+        rows[2, :n] = tables[np.arange(n), pos // bs].astype(np.int64) * bs + pos % bs
+        rows[3, :n] = pos + 1
+        rows[:, n:b] = np.array([[0], [0], [self.scratch_slot], [1]])
+        tables[n:b, 0] = self.scratch_block
+        for dst, src in ((self.input_ids, self._host[0]), (self.positions, self._host[1]),
+                         (self.slots, self._host[2]), (self.ctx, self._host[3])):
+            dst[:b].copy_(src[:b], non_blocking=True)
+        self.tables[:b].copy_(self._host_tables[:b], non_blocking=True)
         self._staged = torch.cuda.Event()
         self._staged.record()
         self.ctx_start[:b].copy_(self.ctx[:b])

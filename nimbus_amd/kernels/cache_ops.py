@@ -9,6 +9,7 @@ from __future__ import annotations
 import torch
 
 from nimbus_amd import _lib
+from nimbus_amd.kernels import index_checks
 
 
 def write_kv(
@@ -23,7 +24,8 @@ def write_kv(
     Same contract as the reference's two index_copy_ calls: the caches must be
     viewable flat (contiguous); k and v may be strided in their first two
     dims (a slice of a fused qkv projection). Slots outside the cache are
-    skipped rather than written.
+    skipped rather than written, unless index checks are on
+    (index_checks: NIMBUS_CHECK_INDICES=1), which raise IndexError first.
     """
     if k.shape != v.shape or k.dim() != 3:
         raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} must both be [T, KV, D]")
@@ -42,6 +44,8 @@ def write_kv(
         raise ValueError("write_kv runs on the GPU only")
     if t == 0:
         return
+    if index_checks.enabled():
+        index_checks.check_slots(slot_mapping, k_cache.shape[0] * k_cache.shape[1])
     if k.stride(-1) != 1:
         k = k.contiguous()
     if v.stride(-1) != 1:

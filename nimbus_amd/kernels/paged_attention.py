@@ -18,6 +18,7 @@ from __future__ import annotations
 import torch
 
 from nimbus_amd import _lib
+from nimbus_amd.kernels import index_checks
 
 PAGE = 16  # tokens per KV-cache block: the only block size the kernels take
 
@@ -118,6 +119,8 @@ def paged_decode_attention(
     context_lens = context_lens.contiguous()
     if block_tables.stride(1) != 1:
         block_tables = block_tables.contiguous()
+    if index_checks.enabled():
+        index_checks.check_tables(block_tables, context_lens, k_cache.shape[0], k_cache.shape[1])
     lib = _lib.load()
     need = lib.nimbus_paged_decode_workspace_bytes(b, h, d, int(max_context))
     if workspace is not None:
@@ -194,6 +197,8 @@ def paged_verify_attention(
     context_lens = context_lens.contiguous()
     if block_tables.stride(1) != 1:
         block_tables = block_tables.contiguous()
+    if index_checks.enabled():
+        index_checks.check_tables(block_tables, context_lens, k_cache.shape[0], k_cache.shape[1])
     lib = _lib.load()
     need = lib.nimbus_paged_verify_workspace_bytes(b, nq, h, d, int(max_context))
     if workspace is not None:

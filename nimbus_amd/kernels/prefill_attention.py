@@ -22,6 +22,7 @@ import numpy as np
 import torch
 
 from nimbus_amd import _lib
+from nimbus_amd.kernels import index_checks
 from nimbus_amd.kernels.paged_attention import (MAX_VERIFY_QUERIES, PAGE, _cached_workspace, _check_cache,
                                                 paged_verify_attention)
 
@@ -173,6 +174,11 @@ def plan_pieces(query_start_host: list[int], context_lens_host: list[int], num_h
     return PrefillPieces(t, mt, slot)
 
 
+def pieces_workspace_bytes(num_slots: int, heads: int, head_dim: int) -> int:
+    """Workspace bytes of a PrefillPieces plan with num_slots split slots."""
+    return int(_lib.load().nimbus_paged_prefill_pieces_workspace_bytes(num_slots, heads, head_dim))
+
+
 def paged_prefill_attention(
     q: torch.Tensor,  # [Tp, H, D]
     k_cache: torch.Tensor,
@@ -232,6 +238,8 @@ def paged_prefill_attention(
     if nq:
         return paged_verify_attention(q, k_cache, v_cache, context_lens, block_tables, nq,
                                       block_tables.shape[1] * PAGE, scale, out=out, workspace=workspace)
+    if index_checks.enabled():
+        index_checks.check_tables(block_tables, context_lens, k_cache.shape[0], k_cache.shape[1])
     if programs is None:
         programs = build_programs(query_start_host, q.device, context_lens_host)
     if q.stride(-1) != 1:

@@ -80,6 +80,26 @@ class AttentionBackend:
         self._prefill = prefill_attention.paged_prefill_attention
         self._build_programs = prefill_attention.build_programs
 
+    def _prefill_workspace(self, meta: AttnMetadata, q: torch.Tensor) -> torch.Tensor | None:
+        """This backend's workspace for a prefill call when it holds what the
+        call needs (the verify form's pieces, or a PrefillPieces plan's
+        slots), else None: the call then takes the per-stream cached
+        workspace. A workspace sized for decode alone (DecodeGraphs gives the
+        model's backend one) can be smaller than a key-range plan of an eager
+        chunked-prefill step needs."""
+        ws = self.decode_workspace
+        if ws is None:
+            return None
+        h, d = q.shape[1], q.shape[2]
+        if meta.prefill_kernel == "verify":
+            need = paged_attention.verify_workspace_bytes(meta.num_prefills, meta.prefill_query_start_host[1], h, d,
+                                                          meta.prefill_block_tables.shape[1] * paged_attention.PAGE)
+        elif isinstance(meta.prefill_programs, prefill_attention.PrefillPieces):
+            need = prefill_attention.pieces_workspace_bytes(meta.prefill_programs.num_slots, h, d)
+        else:
+            return None  # the plain tile table needs no workspace
+        return ws if ws.numel() * ws.element_size() >= need else None
+
     def forward(
         self,
         q: torch.Tensor,  # [T, H, D]
@@ -111,7 +131,7 @@ class AttentionBackend:
                 q[:p], k_cache, v_cache, meta.prefill_query_start, meta.prefill_context_lens,
                 meta.prefill_block_tables, scale, meta.prefill_query_start_host,
                 meta.prefill_context_lens_host, meta.prefill_programs, out=out[:p],
-                workspace=self.decode_workspace, kernel=meta.prefill_kernel,
+                workspace=self._prefill_workspace(meta, q), kernel=meta.prefill_kernel,
             )
         if meta.num_decodes:
             self._decode(

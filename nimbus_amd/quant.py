@@ -1,8 +1,8 @@
 """INT8 weight-only quantization (symmetric, per output channel).
 
-Mirrors nimbus/quant/int8.py:20-71: each weight row gets the scale
-max|row| / 127 and is stored as round(w / scale) in int8; activations stay
-in the model dtype and the scale is applied after the product
+The number format of nimbus/quant/int8.py:20-29: each weight row gets the
+scale max|row| / 127 and is stored as round(w / scale) in int8; activations
+stay in the model dtype and the scale is applied after the product
 (x @ (w_q * s)^T == (x @ w_q^T) * s). Int8Linear runs the HIP kernel
 (kernels/int8_matmul.py); the quantizer itself is host-side set-up run once
 per weight, in PyTorch on whatever device the weight lives.
@@ -58,26 +58,31 @@ class Int8Linear(nn.Module):
         return int8_matmul_packed(x, self.weight_packed, self.scale, self.out_features, self.in_features)
 
 
-QUANTIZED = ("qkv_proj", "o_proj", "gate_up_proj", "down_proj")
+# Attribute names of the decoder's projections (nimbus/model/llama.py): the
+# layers whose weights are quantized. Embeddings, norms and the LM head keep
+# the model dtype, as in the reference (quant/int8.py:50-65).
+PROJECTIONS = frozenset({"qkv_proj", "o_proj", "gate_up_proj", "down_proj"})
 
 
 @torch.no_grad()
 def quantize_model(model: nn.Module, use_hip: bool = True) -> nn.Module:
-    """Replaces the decoder projections (model.layers[i].self_attn / .mlp)
-    with Int8Linear in place (nimbus/quant/int8.py:53-65)."""
-    for layer in model.layers:
-        for parent in (layer.self_attn, layer.mlp):
-            for name in QUANTIZED:
-                lin = getattr(parent, name, None)
-                if isinstance(lin, nn.Linear):
-                    setattr(parent, name, Int8Linear(lin, use_hip))
-                    del lin
-    if torch.cuda.is_available():
-        torch.cuda.empty_cache()
+    """Swaps each plain nn.Linear registered under one of PROJECTIONS for an
+    Int8Linear built from it, in place; returns the model."""
+    swaps = [(owner, name, child) for owner in model.modules() for name, child in owner.named_children()
+             if name in PROJECTIONS and type(child) is nn.Linear]
+    for owner, name, child in swaps:
+        owner.add_module(name, Int8Linear(child, use_hip))
     return model
 
 
 def weight_bytes(model: nn.Module) -> int:
-    """(nimbus/quant/int8.py:68-71)"""
-    return sum(t.numel() * t.element_size() for t in list(model.parameters()) + list(model.buffers())
-               if t.dtype in (torch.float16, torch.bfloat16, torch.float32, torch.int8) and not t.is_meta)
+    """Bytes of the tensors a forward pass reads from the model (parameters
+    and buffers), each storage counted once: tied weights once, the int8
+    projections at one byte an element."""
+    sizes: dict[int, int] = {}
+    for t in (*model.parameters(), *model.buffers()):
+        if t.is_meta:
+            continue
+        key = t.untyped_storage().data_ptr()
+        sizes[key] = max(sizes.get(key, 0), t.untyped_storage().nbytes())
+    return sum(sizes.values())

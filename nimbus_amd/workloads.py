@@ -268,3 +268,93 @@ def prefill_bytes(seqs, heads: int, kv_heads: int, head_dim: int, elem: int = 2)
 
 def write_kv_bytes(tokens: int, kv_heads: int, head_dim: int, elem: int = 2) -> int:
     return 4 * tokens * kv_heads * head_dim * elem + 8 * tokens
+
+
+# ---------------------------------------------------------------- flat steps from sequence states
+
+@dataclass
+class SeqState:
+    """What a forward step reads of a sequence: its tokens so far, how many of
+    them already have K/V in the cache, and its pages. The attribute names are
+    those of Nimbus's Sequence (nimbus/sequence.py), so DecodeGraphs takes
+    either."""
+
+    token_ids: list
+    block_table: list = field(default_factory=list)
+    num_computed: int = 0
+
+    def __len__(self) -> int:
+        return len(self.token_ids)
+
+    def feed(self, token: int) -> None:
+        """Every pending token was computed and `token` was sampled after them."""
+        self.num_computed = len(self.token_ids)
+        self.token_ids.append(int(token))
+
+    def copy(self) -> "SeqState":
+        return SeqState(list(self.token_ids), list(self.block_table), self.num_computed)
+
+
+def is_decode(seq, n: int) -> bool:
+    """A sequence feeding its single last pending token on top of a cached
+    prefix is a decode; anything else is a prefill (possibly a chunk that
+    continues a cached prefix)."""
+    return n == 1 and 0 < seq.num_computed == len(seq) - 1
+
+
+@dataclass
+class FlatStep:
+    input_ids: torch.Tensor  # [T] int64
+    positions: torch.Tensor  # [T] int64
+    meta: object  # model.attention.AttnMetadata
+    sample_rows: torch.Tensor  # [S'] int64: last row of every sequence whose pending tokens this step finishes
+
+
+def flat_step(entries, device, block_size: int = BLOCK_SIZE) -> FlatStep:
+    """One forward pass over `entries` = [(sequence, tokens to feed)], laid out
+    as Nimbus's runner lays it (nimbus/runner.py:33-96): the fed tokens of
+    every sequence back to back, prefills first; token p of a sequence goes to
+    slot table[p // block_size] * block_size + p % block_size; each group's
+    block tables are zero-padded to its widest row."""
+    from nimbus_amd.model.attention import AttnMetadata
+
+    if not entries:
+        raise ValueError("empty step")
+    feed = np.array([n for _, n in entries], dtype=np.int64)
+    start = np.array([s.num_computed for s, _ in entries], dtype=np.int64)
+    end = start + feed
+    if (feed < 1).any() or (end > np.array([len(s) for s, _ in entries])).any():
+        raise ValueError("a sequence is asked for tokens it does not have")
+    dec = np.array([is_decode(s, int(n)) for s, n in entries])
+    if dec.any() and not dec[int(np.argmax(dec)):].all():
+        raise ValueError("prefill sequences must come before decodes")
+    widths = np.array([len(s.block_table) for s, _ in entries], dtype=np.int64)
+    if (widths * block_size < end).any():
+        raise ValueError("a sequence has too few blocks for its tokens")
+    tables = np.zeros((len(entries), max(1, int(widths.max()))), dtype=np.int32)
+    for r, (s, _) in enumerate(entries):
+        tables[r, :widths[r]] = s.block_table
+    row_of = np.repeat(np.arange(len(entries)), feed)
+    first_row = np.cumsum(feed) - feed
+    pos = start[row_of] + np.arange(row_of.size) - first_row[row_of]
+    slots = tables[row_of, pos // block_size].astype(np.int64) * block_size + pos % block_size
+    ids = np.concatenate([np.asarray(s.token_ids[a:b], dtype=np.int64) for (s, _), a, b in zip(entries, start, end)])
+    done = end == np.array([len(s) for s, _ in entries])
+    sample = (first_row + feed - 1)[done]
+
+    def group(mask):
+        w = max(1, int(widths[mask].max())) if mask.any() else 1
+        return torch.from_numpy(np.ascontiguousarray(tables[mask, :w])).to(device)
+
+    pf = ~dec
+    qs_host = [0] + np.cumsum(feed[pf]).tolist()
+    pf_ctx = end[pf].tolist()
+    dc_ctx = end[dec].tolist()
+    dev_i32 = lambda x: torch.tensor(x, dtype=torch.int32).to(device)  # noqa: E731
+    meta = AttnMetadata(
+        slot_mapping=torch.from_numpy(slots).to(device), num_prefill_tokens=qs_host[-1],
+        prefill_query_start=dev_i32(qs_host), prefill_context_lens=dev_i32(pf_ctx), prefill_block_tables=group(pf),
+        decode_context_lens=dev_i32(dc_ctx), decode_block_tables=group(dec), max_decode_context=max(dc_ctx, default=0),
+        prefill_query_start_host=qs_host, prefill_context_lens_host=pf_ctx)
+    return FlatStep(torch.from_numpy(ids).to(device), torch.from_numpy(pos).to(device), meta,
+                    torch.from_numpy(sample).to(device))

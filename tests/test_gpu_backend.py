@@ -51,6 +51,70 @@ def test_mixed_step_matches_oracle():
                   what="decode part")
 
 
+def test_config4_step_with_graph_replayed_decode():
+    """BASELINE config 4 as the bench runs it: the slot write of the prefill
+    tokens and the prefill (eager), then the 60 decodes (contexts U[256,
+    4096]) replayed from DecodeAttentionGraphs padded to 64, whose graph
+    writes the decode tokens' K/V itself. Both parts against the oracle, the
+    cache bit-exact, and every replay (eager work between them) identical."""
+    announce("config 4 step: eager prefill + decode graph padded to 64")
+    from nimbus_amd.kernels.cache_ops import write_kv
+    from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
+
+    ref = workloads.llama3_mixed("cuda")
+    b = workloads.build_batch(ref.seqs, heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16, device="cuda",
+                              seed=0, write_first=False)
+    nb = b.k_cache.shape[0]
+    kc = torch.cat([b.k_cache, torch.zeros_like(b.k_cache[:1])])  # + the scratch block
+    vc = torch.cat([b.v_cache, torch.zeros_like(b.v_cache[:1])])
+    k_before = kc[:nb].clone()
+    graphs = DecodeAttentionGraphs(kc, vc, num_heads=32, scale=b.scale, max_model_len=8192, max_batch=64,
+                                   scratch_block=nb)
+    graphs.capture()
+    p_tok = b.num_prefill_tokens
+    pa, da = b.prefill_args(), b.decode_args()
+    assert len(b.decode_context_host()) == 60
+    write_kv(b.k[:p_tok], b.v[:p_tok], kc, vc, b.slot_mapping[:p_tok])
+    out_p = paged_prefill_attention(pa[0], kc, vc, pa[3], pa[4], pa[5], pa[6], pa[7], pa[8],
+                                    build_programs(pa[7], "cuda", pa[8]))
+    gb = graphs.load(da[0], b.k[p_tok:], b.v[p_tok:], b.slot_mapping[p_tok:], da[3], da[4])
+    assert gb == 64
+    replays = []
+    for _ in range(3):
+        replays.append(graphs.replay(gb)[:60].clone())
+        torch.cuda.synchronize()
+        _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # eager work between replays
+    for r in replays[1:]:
+        assert torch.equal(r, replays[0])
+    kref = k_before.view(-1, 8, 128)
+    kref[b.slot_mapping] = b.k
+    assert torch.equal(kc[:nb].view(-1, 8, 128).view(torch.int16), kref.view(torch.int16))
+    q, _, _, _, _, bt, scale, qs, ctx = b.prefill_args()
+    assert_within(out_p.cpu(), oracle_prefill(q, kc, vc, qs, ctx, bt, scale), what="config 4 prefill part")
+    want = oracle_decode(da[0], kc, vc, b.decode_context_host(), da[4], scale)
+    assert_within(replays[0].cpu(), want, what="config 4 decode part, graph replay at 64")
+
+
+def test_eager_chunked_prefill_after_decode_graph_setup():
+    """A backend holding a workspace sized for decode alone (what DecodeGraphs
+    gives a model's backend: 8 rows up to 8192 tokens) still runs an eager
+    64-token chunk over an 8192-token prefix, whose key-range plan needs more
+    workspace than that, and matches the oracle."""
+    announce("eager chunked prefill through a backend with a decode-sized workspace")
+    from nimbus_amd.kernels.paged_attention import decode_workspace_bytes, new_decode_workspace
+    from nimbus_amd.kernels.prefill_attention import PrefillPieces, pieces_workspace_bytes, plan_pieces
+
+    b = workloads.build_batch([(8192 + 64, 64)], heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16,
+                              device="cuda", seed=4, write_first=False)
+    small = new_decode_workspace(decode_workspace_bytes(8, 32, 128, 8192), "cuda")
+    plan = plan_pieces([0, 64], [8256], 32, 8, "cuda")
+    assert isinstance(plan, PrefillPieces) and pieces_workspace_bytes(plan.num_slots, 32, 128) > small.numel()
+    backend = AttentionBackend(decode_workspace=small)
+    out = backend.forward(b.q, b.k, b.v, b.k_cache, b.v_cache, _meta(b), b.scale)
+    q, k, v, _, _, bt, scale, qs, ctx = b.prefill_args()
+    assert_within(out.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="chunk over an 8192 prefix")
+
+
 @pytest.mark.parametrize("n", [60, 3, 1])
 def test_decode_graph_replay_matches_eager(n):
     """Decode attention captured at padded sizes (padding rows on a scratch

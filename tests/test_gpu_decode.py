@@ -168,17 +168,24 @@ def test_config3_llama3_decode_full():
     assert_within(got.cpu(), want, what="config 3")
 
 
-def test_config5_long_context_sampled_rows():
-    """B=256 with 16k-32k rows in a ~40 GB pool: every long row and a sample of
-    short ones against the oracle; all rows finite."""
+def test_config5_long_context_rows():
+    """B=256 with 16k-32k rows in a ~40 GB pool: every long row and 64 random
+    short rows (plus the first and last rows) against the per-row oracle;
+    all rows finite."""
     announce("decode config llama3_long_decode (40 GB pool)")
+    import numpy as np
+
     b = workloads.llama3_long_decode("cuda")
     args = b.decode_args()
     got = paged_decode_attention(*args)
     torch.cuda.synchronize()
     assert torch.isfinite(got.float()).all()
     lens = b.decode_context_host()
-    rows = [i for i, c in enumerate(lens) if c >= 16384][:12] + [0, 1, 2, 3, 100, 255]
+    long_rows = [i for i, c in enumerate(lens) if c >= 16384]
+    short = [i for i, c in enumerate(lens) if c < 16384]
+    picked = np.random.default_rng(5).choice(short, size=64, replace=False).tolist()
+    rows = sorted(set(long_rows + picked + [0, len(lens) - 1]))
+    assert len(long_rows) >= 10 and len(rows) >= 74
     sel = torch.tensor(rows, device="cuda")
     want = oracle_decode(args[0][sel], b.k_cache, b.v_cache, [lens[i] for i in rows], args[4][sel], b.scale)
     assert_within(got[sel].cpu(), want, what="config 5 rows")

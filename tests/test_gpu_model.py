@@ -29,8 +29,8 @@ from nimbus_amd.kernels.elementwise import greedy_step, rope_, silu_mul
 from nimbus_amd.model.attention import AttnMetadata
 from nimbus_amd.model.config import ModelConfig
 from nimbus_amd.model.llama import build_model
-from nimbus_amd.model.runner import Sequence, prepare
 from nimbus_amd.quant import quantize_model
+from nimbus_amd.workloads import SeqState, flat_step
 from oracle import model as omodel
 from tests.gpu_helpers import announce
 
@@ -51,9 +51,7 @@ def _setup(dtype, prompt_lens, num_blocks=96, seed=0, cfg=CFG):
     seqs = []
     for i, n in enumerate(prompt_lens):
         ids = [rng.randrange(1, cfg.vocab_size) for _ in range(n)]
-        s = Sequence(i, ids)
-        s.block_table = [pool.pop() for _ in range(-(-(n + 24) // BS))]  # room for 24 more tokens
-        seqs.append(s)
+        seqs.append(SeqState(ids, [pool.pop() for _ in range(-(-(n + 24) // BS))]))  # room for 24 more tokens
     return model, caches, seqs
 
 
@@ -66,7 +64,7 @@ def _cpu_meta(meta: AttnMetadata) -> AttnMetadata:
 
 
 def _eager_step(model, caches, batch):
-    step = prepare(batch, BS, "cuda")
+    step = flat_step(batch, "cuda", BS)
     logits = model.logits(model(step.input_ids, step.positions, caches, step.meta))
     return step, logits[step.sample_rows]
 
@@ -88,25 +86,18 @@ def test_model_matches_oracle_prefill_then_decode(dtype, atol):
         announce(f"  step {step_i}: max |logit error| {err:.2e} (logit scale {want.abs().max().item():.2f})")
         assert err <= atol * max(1.0, want.abs().max().item()), err
         for s, tok in zip(seqs, got.argmax(-1).tolist()):  # same inputs for both next step
-            s.num_computed = len(s)
-            s.append(tok)
+            s.feed(tok)
         batch = [(s, 1) for s in seqs]
 
 
 def _prefill(model, caches, seqs):
     _, logits = _eager_step(model, caches, [(s, len(s)) for s in seqs])
     for s, tok in zip(seqs, logits.argmax(-1).tolist()):
-        s.num_computed = len(s)
-        s.append(tok)
+        s.feed(tok)
 
 
 def _clone_seqs(seqs):
-    out = []
-    for s in seqs:
-        c = Sequence(s.seq_id, list(s.prompt_ids), list(s.block_table), s.num_computed)
-        c.token_ids, c.output_ids = list(s.token_ids), list(s.output_ids)
-        out.append(c)
-    return out
+    return [s.copy() for s in seqs]
 
 
 def _clone_caches(caches):
@@ -131,11 +122,9 @@ def test_decode_graphs_match_eager(n, dtype):
         g_tok, e_tok = got.argmax(-1).tolist(), want.argmax(-1).tolist()
         assert g_tok == e_tok, (step_i, g_tok, e_tok)
         for s, t in zip(g_seqs, g_tok):
-            s.num_computed = len(s)
-            s.append(t)
+            s.feed(t)
         for s, t in zip(e_seqs, e_tok):
-            s.num_computed = len(s)
-            s.append(t)
+            s.feed(t)
 
 
 def test_greedy_chain_matches_stepwise_runs():
@@ -156,8 +145,7 @@ def test_greedy_chain_matches_stepwise_runs():
         toks = gb.run(b_seqs).argmax(-1).tolist()
         assert toks == chain[:, k].tolist(), k
         for s, t in zip(b_seqs, toks):
-            s.num_computed = len(s)
-            s.append(t)
+            s.feed(t)
     # both graph paths wrote the same K/V into their caches
     for (ka, va), (kb, vb) in zip(a_caches, b_caches):
         assert torch.equal(ka[:160], kb[:160]) and torch.equal(va[:160], vb[:160])
@@ -180,11 +168,9 @@ def test_int8_model_stays_close():
         assert cos.min().item() > 0.99, cos
         toks = ref.argmax(-1).tolist()  # feed both the unquantized model's tokens
         for s, t in zip(seqs, toks):
-            s.num_computed = len(s)
-            s.append(t)
+            s.feed(t)
         for s, t in zip(q_seqs, toks):
-            s.num_computed = len(s)
-            s.append(t)
+            s.feed(t)
         batch = [(s, 1) for s in seqs]
         q_batch = [(s, 1) for s in q_seqs]
 

@@ -5,7 +5,9 @@ from __future__ import annotations
 
 import dataclasses
 import math
+import os
 
+import numpy as np
 import pytest
 import torch
 
@@ -151,6 +153,71 @@ def test_batch_layout_follows_runner():
     assert da[5] == 100 and da[0].shape == (2, 4, 64)
 
 
+def test_flat_step_follows_runner_layout():
+    """flat_step against the layout contract written out token by token
+    (nimbus/runner.py:33-96): fed tokens back to back, prefills first, slot
+    = table[p // 16] * 16 + p % 16, per-group zero-padded tables, host lists,
+    and the rows sampled (sequences whose pending tokens the step finishes)."""
+    rng = np.random.default_rng(7)
+    fresh = workloads.SeqState(list(rng.integers(0, 99, 23)), [5, 9])
+    chunk = workloads.SeqState(list(rng.integers(0, 99, 70)), [1, 2, 3, 4, 8], num_computed=32)
+    dec_a = workloads.SeqState(list(rng.integers(0, 99, 18)), [7, 6], num_computed=17)
+    dec_b = workloads.SeqState(list(rng.integers(0, 99, 3)), [11], num_computed=2)
+    entries = [(fresh, 23), (chunk, 20), (dec_a, 1), (dec_b, 1)]
+    st = workloads.flat_step(entries, "cpu")
+    ids, pos, slots, sample = [], [], [], []
+    for s, n in entries:
+        for p in range(s.num_computed, s.num_computed + n):
+            ids.append(s.token_ids[p])
+            pos.append(p)
+            slots.append(s.block_table[p // 16] * 16 + p % 16)
+        if s.num_computed + n == len(s):
+            sample.append(len(ids) - 1)
+    assert st.input_ids.tolist() == ids and st.positions.tolist() == pos
+    m = st.meta
+    assert m.slot_mapping.tolist() == slots and m.slot_mapping.dtype == torch.int64
+    assert st.sample_rows.tolist() == sample  # the chunk (52 of 70 done) is not sampled
+    assert m.num_prefill_tokens == 43 and m.prefill_query_start_host == [0, 23, 43]
+    assert m.prefill_context_lens_host == [23, 52] and m.prefill_context_lens.tolist() == [23, 52]
+    assert m.prefill_block_tables.tolist() == [[5, 9, 0, 0, 0], [1, 2, 3, 4, 8]]
+    assert m.decode_context_lens.tolist() == [18, 3] and m.max_decode_context == 18
+    assert m.decode_block_tables.tolist() == [[7, 6], [11, 0]]
+    assert m.decode_block_tables.dtype == torch.int32 and m.num_decodes == 2 and m.num_prefills == 2
+    with pytest.raises(ValueError):
+        workloads.flat_step([(dec_a, 1), (fresh, 23)], "cpu")  # a decode before a prefill
+    with pytest.raises(ValueError):
+        workloads.flat_step([(workloads.SeqState([1] * 40, [3]), 40)], "cpu")  # 40 tokens on one page
+    with pytest.raises(ValueError):
+        workloads.flat_step([(dec_b, 2)], "cpu")  # more tokens than pending
+
+
+def test_flat_step_matches_build_batch():
+    """The two generators of the runner's layout agree: a prefill chunk over
+    a prefix and decodes, with build_batch's tables."""
+    b = workloads.build_batch([(40, 40), (70, 30), (100, 1), (17, 1)], heads=4, kv_heads=2, head_dim=64,
+                              dtype=torch.float16, device="cpu", seed=3)
+    entries = [(workloads.SeqState(list(range(c)), t, c - ql), ql) for (c, ql), t in zip(b.seqs, b.tables_host)]
+    st = workloads.flat_step(entries, "cpu")
+    assert torch.equal(st.meta.slot_mapping, b.slot_mapping)
+    pa, da = b.prefill_args(), b.decode_args()
+    assert st.meta.prefill_query_start_host == pa[7] and st.meta.prefill_context_lens_host == pa[8]
+    assert torch.equal(st.meta.decode_context_lens, da[3])
+    assert st.meta.max_decode_context == da[5]
+
+
+def test_weight_bytes_counts_each_storage_once():
+    from torch import nn
+
+    from nimbus_amd.quant import weight_bytes
+
+    emb = nn.Embedding(10, 4)
+    head = nn.Linear(4, 10, bias=False)
+    head.weight = emb.weight  # tied
+    model = nn.Sequential(emb, nn.Linear(4, 6, bias=False), head)
+    model.register_buffer("table", torch.zeros(3, dtype=torch.float16))
+    assert weight_bytes(model) == 10 * 4 * 4 + 6 * 4 * 4 + 3 * 2
+
+
 def test_pages_are_distinct():
     b = workloads.tinyllama_decode("cpu")
     pages = [p for t in b.tables_host for p in t]
@@ -237,3 +304,25 @@ def test_plan_pieces_declines_when_tiles_fill_the_chip():
     qs4 = [0, 512, 1024, 1536, 2048]  # config 4: 32 tiles fill the chip, two per CU
     assert plan_pieces(qs4, [1512, 529, 1152, 1536], 32, 8, "cpu") is None
     assert plan_pieces([0, 64], [64], 32, 8, "cpu") is None  # one short tile: nothing to cut
+
+
+def test_index_checks_raise_like_the_reference():
+    """The opt-in checks raise IndexError where the reference's index_copy_
+    and table gathers would fail, and pass padding past a row's context."""
+    from nimbus_amd.kernels import index_checks
+
+    index_checks.check_slots(torch.tensor([0, 5, 63]), 64)
+    with pytest.raises(IndexError):
+        index_checks.check_slots(torch.tensor([0, 64]), 64)
+    with pytest.raises(IndexError):
+        index_checks.check_slots(torch.tensor([-1]), 64)
+    bt = torch.tensor([[3, 1, 999], [2, 0, 0]], dtype=torch.int32)  # 999: padding past row 0's 2 pages
+    index_checks.check_tables(bt, torch.tensor([20, 16], dtype=torch.int32), 4, 16)
+    with pytest.raises(IndexError):  # row 0 now reads its third page, id 999
+        index_checks.check_tables(bt, torch.tensor([40, 16], dtype=torch.int32), 4, 16)
+    with pytest.raises(IndexError):  # 4 pages needed, table 3 wide
+        index_checks.check_tables(bt, torch.tensor([20, 49], dtype=torch.int32), 4, 16)
+    with pytest.raises(IndexError):
+        index_checks.check_tables(torch.tensor([[-2]], dtype=torch.int32), torch.tensor([1], dtype=torch.int32),
+                                  4, 16)
+    assert not index_checks.enabled() or os.environ.get("NIMBUS_CHECK_INDICES")
