@@ -90,6 +90,8 @@ def parse(argv=None):
     ap.add_argument("--all", action="store_true", help="also time every BASELINE config")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="the headline, then the other decode configs (1 and 5) only: for kernel traces")
     ap.add_argument("--cpu-seconds", type=float, default=25.0, help="bound on the CPU baseline's timed work")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB 5 times (the reference kernel for scaling "
@@ -788,7 +790,7 @@ def reference_shapes(reps=200, warmup=25):
 
 # ---------------------------------------------------------------- configs 1, 2 and 5
 
-def other_configs(steps, warmup):
+def other_configs(steps, warmup, prefill=True):
     """BASELINE configs 1 (TinyLlama decode), 2 (TinyLlama varlen prefill)
     and 5 (long-context decode, ~40 GB pool) in compact form: µs per call of
     back-to-back calls, GB/s or TFLOP/s and the roofline fraction."""
@@ -810,6 +812,8 @@ def other_configs(steps, warmup):
         }
         del b
         torch.cuda.empty_cache()
+    if not prefill:
+        return rows
     log("config 2 (tinyllama_prefill)")
     b = workloads.CONFIGS["tinyllama_prefill"]("cuda")
     r = time_prefill(b, steps, warmup)
@@ -919,6 +923,9 @@ def main(argv=None):
             "merge_pass_share_us": dec["merge_us"],
         },
     }
+    if args.decode_only:
+        args.no_prefill = True
+        result["other_configs"] = other_configs(min(args.steps, 50), args.warmup, prefill=False)
     if not args.no_prefill:
         log("building llama3_mixed (config 4)")
         mixed = workloads.llama3_mixed("cuda")

@@ -56,9 +56,10 @@ __device__ __forceinline__ uint16_t f32_to_f16(float f) {
 // P lies in [0, 256], where fp16 keeps 3 more mantissa bits than bf16
 // (rounding P to bf16 alone costs ~8e-3 at |o| ~ 0.5, beyond the output
 // tolerance), and a finite bf16 V element converts to fp16 exactly when
-// 2^-14 <= |v| <= 65504 (fp16's normal range). Smaller magnitudes become
-// fp16 subnormals, with an absolute error below 2^-24 (values below 2^-24
-// flush to zero), so relative accuracy falls for very small V. The
+// 2^-17 <= |v| <= 65504 (fp16 subnormals keep bf16's 8 significant bits
+// down to 2^-17). Smaller magnitudes lose bits, with an absolute error below
+// 2^-24 (values below 2^-24 flush to zero), so relative accuracy falls for
+// very small V. The
 // conversion rounds toward zero, so larger finite |v| saturate to +-65504
 // rather than becoming inf, and one outlier cannot turn masked-out products
 // (0 * inf) into NaN for other rows. (Decode, which
