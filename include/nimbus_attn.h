@@ -41,6 +41,7 @@ extern "C" {
 #define NIMBUS_ERR_UNSUPPORTED (-2) /* shape/dtype outside what the kernels cover */
 #define NIMBUS_ERR_ALIGNMENT (-3)   /* a base or stride breaks 16-byte vector access */
 #define NIMBUS_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+#define NIMBUS_ERR_SCRATCH (-5)     /* call needs more than nimbus_paged_decode_noalloc's scratch */
 
 /* Version of this ABI (NIMBUS_ATTN_ABI_VERSION). */
 int nimbus_attn_abi_version(void);
@@ -124,6 +125,28 @@ int nimbus_paged_decode_merge(const void* q, int64_t q_stride_b, int64_t q_strid
                               int64_t out_stride_b, int64_t out_stride_h, void* workspace, int64_t workspace_bytes,
                               int32_t batch, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                               int32_t block_size, int64_t max_context, float scale, int32_t dtype, void* stream);
+
+/*
+ * Allocation-free paged decode. No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under hipGraph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments and
+ * results as nimbus_paged_decode without the workspace: the kernels use a
+ * device array of NIMBUS_NOALLOC_SCRATCH_BYTES inside the library instead,
+ * one per device, held until the process ends (its address is looked up
+ * once per device, on the first call there). A call whose workspace
+ * (nimbus_paged_decode_workspace_bytes) exceeds it returns
+ * NIMBUS_ERR_SCRATCH without launching. Every call on a device shares that
+ * device's array, so calls that overlap on one device (concurrent streams)
+ * race: serialise them. Nothing in the array carries over between calls.
+ */
+#define NIMBUS_NOALLOC_SCRATCH_BYTES (64LL << 20)
+int nimbus_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+                                const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                                int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                                int64_t bt_stride, int32_t bt_width, const int32_t* context_lens, void* out,
+                                int64_t out_stride_b, int64_t out_stride_h, int32_t batch, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int64_t max_context,
+                                float scale, int32_t dtype, void* stream);
 
 /*
  * Causal varlen paged prefill attention. Replaces

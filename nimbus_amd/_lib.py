@@ -25,6 +25,8 @@ NIMBUS_ERR_INVALID = -1
 NIMBUS_ERR_UNSUPPORTED = -2
 NIMBUS_ERR_ALIGNMENT = -3
 NIMBUS_ERR_WORKSPACE = -4
+NIMBUS_ERR_SCRATCH = -5
+NOALLOC_SCRATCH_BYTES = 64 << 20  # NIMBUS_NOALLOC_SCRATCH_BYTES
 ABI_VERSION = 10
 
 # Entry points and their C signatures, in the order include/nimbus_attn.h declares them.
@@ -40,6 +42,9 @@ SIGNATURES = {
                                      _c_i32, _c_i64, _c_f, _c_i32, _c_p]),
     "nimbus_paged_decode_pages": None,
     "nimbus_paged_decode_merge": None,
+    "nimbus_paged_decode_noalloc": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p,
+                                             _c_i64, _c_i32, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32,
+                                             _c_i32, _c_i32, _c_i64, _c_f, _c_i32, _c_p]),
     "nimbus_paged_prefill": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p, _c_i64,
                                       _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_i64, _c_i64, _c_i32, _c_i32,
                                       _c_i32, _c_i32, _c_f, _c_i32, _c_p]),

@@ -54,6 +54,7 @@
 // the device's CU count), so a call is capturable in a hipGraph, and no
 // workgroup is launched beyond what the chip holds at once.
 #include <atomic>
+#include <mutex>
 
 #include "common.h"
 #include "nimbus_attn_internal.h"
@@ -780,6 +781,66 @@ extern "C" int nimbus_paged_decode_pages(NIMBUS_DECODE_PARAMS) {
 
 extern "C" int nimbus_paged_decode_merge(NIMBUS_DECODE_PARAMS) {
   return paged_decode_impl(2, 1, NIMBUS_DECODE_ARGS);
+}
+
+// ---------------------------------------------------------------- allocation-free decode
+//
+// nimbus_paged_decode_noalloc runs nimbus_paged_decode's kernels with their
+// workspace in `scratch`, a file-scope device array of kNoAllocScratchBytes:
+// each device the library runs on holds its own copy until the process
+// ends, and every call on that device shares it. In host code `scratch`
+// names a host-side stand-in, not device memory: the device address comes
+// from hipGetSymbolAddress, asked once per device (with that device
+// current) on the entry point's first call there, and only that address is
+// handed to kernels. The decode workspace needs no initialisation (the page
+// pass writes the prefix sum and every piece before the merge reads them),
+// so nothing is cleared. Calls that overlap on one device race on it.
+constexpr int64_t kNoAllocScratchBytes = NIMBUS_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::atomic<void*> g_scratch_addr[kMaxDevices];  // null: not asked yet
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch`.
+static int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return NIMBUS_ERR_UNSUPPORTED;
+  void* p = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (p == nullptr) {
+      e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      if (p == nullptr) return static_cast<int>(hipErrorInvalidSymbol);
+      g_scratch_addr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return 0;
+}
+
+extern "C" int nimbus_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                           const void* k_cache, const void* v_cache, int64_t num_blocks,
+                                           int64_t cache_stride_block, int64_t cache_stride_token,
+                                           int64_t cache_stride_head, const int32_t* block_tables, int64_t bt_stride,
+                                           int32_t bt_width, const int32_t* context_lens, void* out,
+                                           int64_t out_stride_b, int64_t out_stride_h, int32_t batch,
+                                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                           int32_t block_size, int64_t max_context, float scale, int32_t dtype,
+                                           void* stream) {
+  const int64_t need = workspace_size(batch, num_heads, head_dim, max_context, 1);
+  if (need < 0) return NIMBUS_ERR_INVALID;
+  if (need > kNoAllocScratchBytes) return NIMBUS_ERR_SCRATCH;
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != 0) return rc;
+  return paged_decode_impl(3, 1, q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks, cache_stride_block,
+                           cache_stride_token, cache_stride_head, block_tables, bt_stride, bt_width, context_lens,
+                           out, out_stride_b, out_stride_h, ws, kNoAllocScratchBytes, batch, num_heads, num_kv_heads,
+                           head_dim, block_size, max_context, scale, dtype, stream);
 }
 
 // q and out hold batch * queries_per_seq tokens in sequence order (token

@@ -79,6 +79,9 @@ extern "C" const char* nimbus_attn_error_string(int code) {
       return "a base pointer or stride breaks 16-byte vector access";
     case NIMBUS_ERR_WORKSPACE:
       return "workspace missing or smaller than the entry point's *_workspace_bytes()";
+    case NIMBUS_ERR_SCRATCH:
+      return "the call needs more workspace than nimbus_paged_decode_noalloc's scratch "
+             "(NIMBUS_NOALLOC_SCRATCH_BYTES); use nimbus_paged_decode with a workspace";
     default:
       return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
   }

@@ -215,3 +215,47 @@ def paged_verify_attention(
         _lib.dtype_code(q.dtype), _lib.stream_of(q))
     _lib.check(rc, "nimbus_paged_verify")
     return out
+
+
+def paged_decode_attention_noalloc(
+    q: torch.Tensor,  # [B, H, D], unit last stride
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    context_lens: torch.Tensor,  # [B] int32, contiguous
+    block_tables: torch.Tensor,  # [B, max_blocks] int32, unit stride along a row
+    max_context: int,
+    scale: float,
+    out: torch.Tensor,  # [B, H, D], unit last stride
+) -> torch.Tensor:
+    """paged_decode_attention without any device allocation, for callers
+    that cannot allocate (nimbus_paged_decode_noalloc): the workspace is a
+    device array inside the library, one per device, shared by every call
+    on it, so calls that overlap on one device (several streams) race.
+    Inputs must already be in the layout the kernels read and `out` must be
+    given: nothing is copied or allocated here. A call needing more
+    workspace than the array holds (_lib.NOALLOC_SCRATCH_BYTES; config 3
+    needs ~35 MB of its 64 MiB) raises ValueError without launching."""
+    if q.dim() != 3 or out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("q and out must both be [B, H, D] of one dtype")
+    b, h, d = q.shape
+    _check_cache(k_cache, v_cache)
+    kv = k_cache.shape[2]
+    if k_cache.shape[3] != d or h % kv != 0 or q.dtype != k_cache.dtype:
+        raise ValueError(f"q {tuple(q.shape)} {q.dtype} does not fit caches {tuple(k_cache.shape)}")
+    if q.stride(-1) != 1 or out.stride(-1) != 1 or not context_lens.is_contiguous() or block_tables.stride(1) != 1:
+        raise ValueError("q/out need unit last stride, context_lens contiguity and block-table rows unit stride "
+                         "(the allocation-free call copies nothing)")
+    if context_lens.dtype != torch.int32 or block_tables.dtype != torch.int32:
+        raise ValueError("context_lens and block_tables must be int32")
+    if context_lens.shape != (b,) or block_tables.dim() != 2 or block_tables.shape[0] != b:
+        raise ValueError("context_lens must be [B] and block_tables [B, max_blocks]")
+    if b == 0:
+        return out
+    lib = _lib.load()
+    rc = lib.nimbus_paged_decode_noalloc(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
+        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(), block_tables.stride(0),
+        block_tables.shape[1], context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1), b, h, kv, d,
+        k_cache.shape[1], int(max_context), float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, "nimbus_paged_decode_noalloc")
+    return out

@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol():
 def test_abi_version_and_error_strings():
     lib = _lib.load()
     assert lib.nimbus_attn_abi_version() == _lib.ABI_VERSION
-    for code in (0, -1, -2, -3, -4):
+    for code in (0, -1, -2, -3, -4, -5):
         assert lib.nimbus_attn_error_string(code)
     assert b"unknown" in lib.nimbus_attn_error_string(-99)
 
