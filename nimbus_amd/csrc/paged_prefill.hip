@@ -474,6 +474,19 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // reads any more); let them land before the workgroup's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
+  // The output rows' heads and bounds again, from a copy of the lane index
+  // the compiler cannot see through: keeping the prologue's values alive
+  // across the walk would cost registers the walk needs.
+  int lane_e = lane;
+  asm volatile("" : "+v"(lane_e));
+  const int col_e = lane_e % 16;
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb) {
+    const int r = 32 * wave + 16 * nb + col_e;
+    row_ok[nb] = m0 + r / GS < q_len;
+    head[nb] = kvh * a.G + gsub * GS + r % GS;
+  }
+
   if (slot >= 0) {
     if (slot >= a.slots) return;
     // A piece: unnormalised O^T, the running max and the row sum, per row
@@ -482,7 +495,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       if (!row_ok[nb]) continue;
-      const int pos = m0 - m_entry + (32 * wave + 16 * nb + col) / GS;
+      const int pos = m0 - m_entry + (32 * wave + 16 * nb + col_e) / GS;
       const int64_t row = (static_cast<int64_t>(slot) * kPrefillTile + pos) * a.H + head[nb];
       float* po = a.part + row * D;
 #pragma unroll
@@ -496,7 +509,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   for (int nb = 0; nb < 2; ++nb) {
     if (!row_ok[nb]) continue;
     const float inv = 1.f / lsum[nb][0];
-    const int pos = (32 * wave + 16 * nb + col) / GS;
+    const int pos = (32 * wave + 16 * nb + col_e) / GS;
     uint16_t* orow = a.out + static_cast<int64_t>(qs + m0 + pos) * a.o_st + static_cast<int64_t>(head[nb]) * a.o_sh;
 #pragma unroll
     for (int nd = 0; nd < ND; ++nd) {

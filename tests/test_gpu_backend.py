@@ -96,17 +96,18 @@ def test_config4_step_with_graph_replayed_decode():
 
 
 def test_eager_chunked_prefill_after_decode_graph_setup():
-    """A backend holding a workspace sized for decode alone (what DecodeGraphs
-    gives a model's backend: 8 rows up to 8192 tokens) still runs an eager
-    64-token chunk over an 8192-token prefix, whose key-range plan needs more
-    workspace than that, and matches the oracle."""
+    """A backend holding a workspace sized for decode alone (DecodeGraphs gives
+    a model's backend one sized for its largest batch, here 2 rows up to 8192
+    tokens) still runs an eager 64-token chunk over an 8192-token prefix,
+    whose key-range plan needs more workspace than that, and matches the
+    oracle."""
     announce("eager chunked prefill through a backend with a decode-sized workspace")
     from nimbus_amd.kernels.paged_attention import decode_workspace_bytes, new_decode_workspace
     from nimbus_amd.kernels.prefill_attention import PrefillPieces, pieces_workspace_bytes, plan_pieces
 
     b = workloads.build_batch([(8192 + 64, 64)], heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16,
                               device="cuda", seed=4, write_first=False)
-    small = new_decode_workspace(decode_workspace_bytes(8, 32, 128, 8192), "cuda")
+    small = new_decode_workspace(decode_workspace_bytes(2, 32, 128, 8192), "cuda")
     plan = plan_pieces([0, 64], [8256], 32, 8, "cuda")
     assert isinstance(plan, PrefillPieces) and pieces_workspace_bytes(plan.num_slots, 32, 128) > small.numel()
     backend = AttentionBackend(decode_workspace=small)
