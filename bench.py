@@ -184,6 +184,32 @@ def event_times_us(fn, steps, stream):
     return [a.elapsed_time(b) * 1e3 for a, b in evs]
 
 
+def graph_us(fn, calls, stream, reps=7):
+    """Captures fn(i) for i < calls into one hipGraph, replays it (3 untimed,
+    then `reps` timed replays, one HIP event pair each on `stream`) and returns
+    the median time per call in microseconds: the device's time per call with
+    no host launch cost between calls, as a serving loop replays decode."""
+    import torch
+
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(calls):
+            fn(i)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        g.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) * 1e3 / calls)
+    del g
+    return statistics.median(times)
+
+
 def rotated_pools(batch, min_bytes=ROTATE_BYTES):
     """Copies of (q, k_cache, v_cache) so that consecutive calls read
     distinct memory; the first copy is the batch's own."""
@@ -241,6 +267,8 @@ def time_decode(batch, steps, warmup, wall=True):
                                                                      steps, stream))
     # the merge pass's share of a call (timed alone, a 5 us launch is bound by the host's launch rate)
     res["merge_us"] = res["call_us"] - res["page_pass_us"]
+    # back-to-back calls replayed from one hipGraph (cycling the pools): no host launch cost
+    res["call_us_graph"] = graph_us(call, max(len(pools), min(12, steps)), stream)
     res["bytes"] = workloads.decode_bytes(ctx_lens, h, kv, d, batch.q.element_size())
     res["pools"] = len(pools)
     res["batch"] = b
@@ -796,7 +824,9 @@ def reference_shapes(reps=200, warmup=25):
 def other_configs(steps, warmup, prefill=True):
     """BASELINE configs 1 (TinyLlama decode), 2 (TinyLlama varlen prefill)
     and 5 (long-context decode, ~40 GB pool) in compact form: µs per call of
-    back-to-back calls, GB/s or TFLOP/s and the roofline fraction."""
+    back-to-back calls (decode: also replayed from a hipGraph, which drops the
+    ~15 µs of host work per eager call that bounds config 1), GB/s or TFLOP/s
+    and the roofline fraction."""
     import torch
 
     from nimbus_amd import workloads
@@ -808,8 +838,9 @@ def other_configs(steps, warmup, prefill=True):
         r = time_decode(b, steps, warmup, wall=False)
         rows[f"config{cfg}"] = {
             "workload": name, "batch": r["batch"], "sum_ctx": r["sum_ctx"], "bytes": r["bytes"],
-            "us_per_call": r["call_us"], "page_pass_us": r["page_pass_us"],
+            "us_per_call": r["call_us"], "us_per_call_graph": r["call_us_graph"], "page_pass_us": r["page_pass_us"],
             "GBps_call": r["bytes"] / r["call_us"] / 1e3,
+            "GBps_call_graph": r["bytes"] / r["call_us_graph"] / 1e3,
             "frac_hbm_peak_call": r["bytes"] / r["call_us"] / 1e3 / HBM_PEAK_GBS,
             "frac_hbm_peak_page_pass": r["bytes"] / r["page_pass_us"] / 1e3 / HBM_PEAK_GBS,
         }
@@ -926,6 +957,7 @@ def main(argv=None):
             "traffic": measured_traffic(dec["bytes"]),
             "kernel_us": dec["call_us"],
             "kernel_us_event_pairs": dec["call_us_event_pairs"],
+            "kernel_us_graph": dec["call_us_graph"],
             "page_pass": {"kernel": "paged_decode_kernel", "us": dec["page_pass_us"],
                           "us_event_pairs": dec["page_pass_us_event_pairs"], "achieved": part_gbs,
                           "frac": part_gbs / HBM_PEAK_GBS},

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 10
+#define NIMBUS_ATTN_ABI_VERSION 11
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -316,6 +316,25 @@ int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* 
 int nimbus_rope(void* x, int64_t x_stride, int64_t num_tokens, int32_t num_heads, int32_t head_dim,
                 const int64_t* positions, const float* cos_table, const float* sin_table, int64_t table_stride,
                 int32_t max_position, int32_t dtype, void* stream);
+
+/*
+ * Rotary embedding and KV slot write in one launch: exactly nimbus_rope(qkv,
+ * qkv_stride, num_tokens, num_heads + num_kv_heads, head_dim, ...) followed
+ * by nimbus_write_kv of the k and v heads of the same rows, bit for bit.
+ * Replaces the rotary of Attention.forward (nimbus/model/llama.py:88-98)
+ * and the write_kv call that AttentionBackend.forward makes first
+ * (nimbus/model/attention.py:78). Row t of qkv (row stride qkv_stride
+ * elements) holds num_heads q heads, then num_kv_heads k heads, then
+ * num_kv_heads v heads, head_dim elements each; the q and k heads are
+ * rotated in place, and the rotated k heads and the v heads go to flat
+ * slot slot_mapping[t] of the contiguous caches [num_slots, num_kv_heads,
+ * head_dim] (slots outside [0, num_slots) skipped, as nimbus_write_kv).
+ * Same alignment rules as nimbus_rope, plus 16-byte aligned caches.
+ */
+int nimbus_rope_write_kv(void* qkv, int64_t qkv_stride, int64_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                         int32_t head_dim, const int64_t* positions, const float* cos_table, const float* sin_table,
+                         int64_t table_stride, int32_t max_position, void* k_cache, void* v_cache,
+                         const int64_t* slot_mapping, int64_t num_slots, int32_t dtype, void* stream);
 
 /*
  * SiLU-gated product of the MLP. Replaces F.silu(gate) * up

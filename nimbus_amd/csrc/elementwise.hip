@@ -10,6 +10,12 @@
 // the result is the reference's bit for bit. It runs in place on the q and k
 // parts of the fused qkv projection (one launch for both).
 //
+// nimbus_rope_write_kv is nimbus_rope on the q and k heads of the fused qkv
+// rows followed by nimbus_write_kv of their k and v heads (the model's
+// Attention.forward then AttentionBackend.forward, nimbus/model/llama.py:
+// 88-98 and nimbus/model/attention.py:78), in one launch and with the same
+// results bit for bit.
+//
 // nimbus_silu_mul replaces MLP.forward's F.silu(gate) * up
 // (nimbus/model/llama.py:93-103): silu in fp32 rounded to the model dtype,
 // then the product rounded again.
@@ -39,30 +45,14 @@ __device__ __forceinline__ float rnd(float v) {
   return Elem<DT>::to_f32(Elem<DT>::from_f32(v));
 }
 
-// One thread per (token, head, 8 consecutive i < D/2): 16-byte loads of x at
-// i and i + D/2.
+// Rotates 8 pairs of one head: lo holds x[i0 .. i0 + 8), hi holds
+// x[i0 + D/2 .. + 8), cr / sr point at the position's table rows.
 template <int DT>
-__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+__device__ __forceinline__ void rope_pairs(u32x4& lo, u32x4& hi, const float* cr, const float* sr, int i0, int half) {
   // The products are rounded before the add; a fused multiply-add would skip
   // that rounding (hipcc contracts by default).
 #pragma clang fp contract(off)
-  const int half = a.d / 2;
-  const int per_head = half / 8;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(a.tokens) * a.heads * per_head;
-  if (idx >= total) return;
-  const int c = static_cast<int>(idx % per_head);
-  const int h = static_cast<int>((idx / per_head) % a.heads);
-  const int64_t t = idx / (static_cast<int64_t>(per_head) * a.heads);
-  const int64_t p = a.pos[t];
-  if (p < 0 || p >= a.max_pos) return;  // no table row: left as is
-  const int i0 = 8 * c;
-  uint16_t* row = a.x + t * a.sx + static_cast<int64_t>(h) * a.d;
-  const u32x4 lo = *reinterpret_cast<const u32x4*>(row + i0);
-  const u32x4 hi = *reinterpret_cast<const u32x4*>(row + half + i0);
   // The table rows' 8 entries at i0 and at i0 + D/2, as 16-byte loads.
-  const float* cr = a.cos + p * a.st;
-  const float* sr = a.sin + p * a.st;
   float c_lo[8], s_lo[8], c_hi[8], s_hi[8];
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
@@ -89,8 +79,79 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
     olo[e] = pack2(out_lo[0], out_lo[1]);
     ohi[e] = pack2(out_hi[0], out_hi[1]);
   }
-  *reinterpret_cast<u32x4*>(row + i0) = olo;
-  *reinterpret_cast<u32x4*>(row + half + i0) = ohi;
+  lo = olo;
+  hi = ohi;
+}
+
+// One thread per (token, head, 8 consecutive i < D/2): 16-byte loads of x at
+// i and i + D/2.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+  const int half = a.d / 2;
+  const int per_head = half / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(a.tokens) * a.heads * per_head;
+  if (idx >= total) return;
+  const int c = static_cast<int>(idx % per_head);
+  const int h = static_cast<int>((idx / per_head) % a.heads);
+  const int64_t t = idx / (static_cast<int64_t>(per_head) * a.heads);
+  const int64_t p = a.pos[t];
+  if (p < 0 || p >= a.max_pos) return;  // no table row: left as is
+  const int i0 = 8 * c;
+  uint16_t* row = a.x + t * a.sx + static_cast<int64_t>(h) * a.d;
+  u32x4 lo = *reinterpret_cast<const u32x4*>(row + i0);
+  u32x4 hi = *reinterpret_cast<const u32x4*>(row + half + i0);
+  rope_pairs<DT>(lo, hi, a.cos + p * a.st, a.sin + p * a.st, i0, half);
+  *reinterpret_cast<u32x4*>(row + i0) = lo;
+  *reinterpret_cast<u32x4*>(row + half + i0) = hi;
+}
+
+struct RopeWriteArgs {
+  RopeArgs r;  // x = the qkv rows, heads = q heads + kv heads (the rotated ones)
+  int32_t q_heads, kv_heads;
+  uint16_t* kc;
+  uint16_t* vc;
+  const int64_t* slots;
+  int64_t num_slots;
+};
+
+// nimbus_rope over the q and k heads, then nimbus_write_kv of the k and v
+// heads, in one launch: one thread per (token, q / k head, 8 pairs). A k
+// head's thread also stores its rotated 16-byte pieces into the K cache
+// slot and copies the same two pieces of the token's v head into the V
+// cache slot.
+template <int DT>
+__global__ __launch_bounds__(256) void rope_write_kv_kernel(RopeWriteArgs w) {
+  const RopeArgs& a = w.r;
+  const int half = a.d / 2;
+  const int per_head = half / 8;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t total = static_cast<int64_t>(a.tokens) * a.heads * per_head;
+  if (idx >= total) return;
+  const int c = static_cast<int>(idx % per_head);
+  const int h = static_cast<int>((idx / per_head) % a.heads);
+  const int64_t t = idx / (static_cast<int64_t>(per_head) * a.heads);
+  const int64_t p = a.pos[t];
+  const bool rotate = p >= 0 && p < a.max_pos;  // no table row: left as is
+  const int i0 = 8 * c;
+  uint16_t* row = a.x + t * a.sx + static_cast<int64_t>(h) * a.d;
+  u32x4 lo = *reinterpret_cast<const u32x4*>(row + i0);
+  u32x4 hi = *reinterpret_cast<const u32x4*>(row + half + i0);
+  if (rotate) {
+    rope_pairs<DT>(lo, hi, a.cos + p * a.st, a.sin + p * a.st, i0, half);
+    *reinterpret_cast<u32x4*>(row + i0) = lo;
+    *reinterpret_cast<u32x4*>(row + half + i0) = hi;
+  }
+  const int kh = h - w.q_heads;
+  if (kh < 0) return;
+  const int64_t slot = w.slots[t];
+  if (slot < 0 || slot >= w.num_slots) return;
+  const int64_t dst = (slot * w.kv_heads + kh) * a.d;
+  *reinterpret_cast<u32x4*>(w.kc + dst + i0) = lo;
+  *reinterpret_cast<u32x4*>(w.kc + dst + half + i0) = hi;
+  const uint16_t* vrow = row + static_cast<int64_t>(w.kv_heads) * a.d;  // v head kh follows the k heads
+  *reinterpret_cast<u32x4*>(w.vc + dst + i0) = *reinterpret_cast<const u32x4*>(vrow + i0);
+  *reinterpret_cast<u32x4*>(w.vc + dst + half + i0) = *reinterpret_cast<const u32x4*>(vrow + half + i0);
 }
 
 struct SiluArgs {
@@ -285,6 +346,55 @@ extern "C" int nimbus_rope(void* x, int64_t x_stride, int64_t num_tokens, int32_
     hipLaunchKernelGGL((rope_kernel<kFloat16>), grid, dim3(256), 0, s, a);
   } else {
     hipLaunchKernelGGL((rope_kernel<kBFloat16>), grid, dim3(256), 0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+extern "C" int nimbus_rope_write_kv(void* qkv, int64_t qkv_stride, int64_t num_tokens, int32_t num_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, const int64_t* positions,
+                                    const float* cos_table, const float* sin_table, int64_t table_stride,
+                                    int32_t max_position, void* k_cache, void* v_cache, const int64_t* slot_mapping,
+                                    int64_t num_slots, int32_t dtype, void* stream) {
+  if (num_tokens < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_position <= 0 ||
+      num_slots < 0)
+    return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (head_dim % 16 != 0 || num_tokens > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return NIMBUS_OK;
+  if (!qkv || !positions || !cos_table || !sin_table || !k_cache || !v_cache || !slot_mapping)
+    return NIMBUS_ERR_INVALID;
+  const int64_t row = (static_cast<int64_t>(num_heads) + 2 * num_kv_heads) * head_dim;
+  if (qkv_stride < row || table_stride < head_dim) return NIMBUS_ERR_INVALID;
+  if (qkv_stride % 8 != 0 || (reinterpret_cast<uintptr_t>(qkv) | reinterpret_cast<uintptr_t>(k_cache) |
+                              reinterpret_cast<uintptr_t>(v_cache)) % 16 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
+  if (table_stride % 4 != 0 ||
+      (reinterpret_cast<uintptr_t>(cos_table) | reinterpret_cast<uintptr_t>(sin_table)) % 16 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
+  RopeWriteArgs w;
+  w.r.x = static_cast<uint16_t*>(qkv);
+  w.r.sx = qkv_stride;
+  w.r.pos = positions;
+  w.r.cos = cos_table;
+  w.r.sin = sin_table;
+  w.r.st = table_stride;
+  w.r.tokens = static_cast<int32_t>(num_tokens);
+  w.r.heads = num_heads + num_kv_heads;
+  w.r.d = head_dim;
+  w.r.max_pos = max_position;
+  w.q_heads = num_heads;
+  w.kv_heads = num_kv_heads;
+  w.kc = static_cast<uint16_t*>(k_cache);
+  w.vc = static_cast<uint16_t*>(v_cache);
+  w.slots = slot_mapping;
+  w.num_slots = num_slots;
+  const int64_t threads = num_tokens * w.r.heads * (head_dim / 16);
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == kFloat16) {
+    hipLaunchKernelGGL((rope_write_kv_kernel<kFloat16>), grid, dim3(256), 0, s, w);
+  } else {
+    hipLaunchKernelGGL((rope_write_kv_kernel<kBFloat16>), grid, dim3(256), 0, s, w);
   }
   return static_cast<int>(hipGetLastError());
 }

@@ -109,11 +109,16 @@ class AttentionBackend:
         v_cache: torch.Tensor,
         meta: AttnMetadata,
         scale: float,
+        kv_written: bool = False,
     ) -> torch.Tensor:
         """write_kv, then prefill on q[:p], then decode on q[p:] (the order of
         model/attention.py:78-94). Both kernels write straight into their
-        slice of the output instead of copying a temporary into it."""
-        cache_ops.write_kv(k, v, k_cache, v_cache, meta.slot_mapping)
+        slice of the output instead of copying a temporary into it.
+        kv_written (not in the reference): the caller has already written k
+        and v into the cache slots (cache_ops.rope_write_kv), so the write
+        is skipped."""
+        if not kv_written:
+            cache_ops.write_kv(k, v, k_cache, v_cache, meta.slot_mapping)
         out = torch.empty_like(q)
         p = meta.num_prefill_tokens
         if p:

@@ -6,7 +6,8 @@ self_attn.o_proj, post_attention_layernorm, mlp.gate_up_proj,
 mlp.down_proj}, norm, lm_head), so a state dict built for Nimbus loads here.
 What runs is this build's GPU path: the HIP RMSNorm / fused add + RMSNorm,
 the HIP rotary embedding applied in place to the q and k heads of the fused
-qkv projection, the paged attention backend, the HIP SiLU gate, and the
+qkv projection in the same launch that writes the KV cache, the paged
+attention backend, the HIP SiLU gate, and the
 projections as torch (hipBLASLt) matmuls or, after quant.quantize_model,
 the HIP INT8 matmul. Numerics follow the reference's: RoPE tables in fp32
 rounded to the model dtype, RMSNorm in fp32, everything else in the model
@@ -20,6 +21,7 @@ import math
 import torch
 from torch import nn
 
+from nimbus_amd.kernels import cache_ops
 from nimbus_amd.kernels.elementwise import rope_, silu_mul
 from nimbus_amd.kernels.rmsnorm import add_rms_norm, rms_norm
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
@@ -100,17 +102,20 @@ class Attention(nn.Module):
         self.backend = backend
 
     def forward(self, x, positions, rotary: Rotary, k_cache, v_cache, meta: AttnMetadata):
-        """nimbus/model/llama.py:88-98. The q and k heads sit side by side in
-        each qkv row, so one in-place rotary launch covers both; q, k and v
-        go to the backend as strided views (no copies)."""
+        """nimbus/model/llama.py:88-98. One launch rotates the q and k heads
+        of each qkv row in place and writes the k and v heads into the cache
+        (the backend's first step, nimbus/model/attention.py:78), so the
+        backend is told the cache already holds them; q goes to it as a
+        strided view (no copy)."""
         t = x.shape[0]
         hd, kvd = self.h * self.d, self.kv * self.d
         qkv = self.qkv_proj(x)
-        rotary.apply_(qkv, self.h + self.kv, positions)
+        cache_ops.rope_write_kv(qkv, self.h, self.kv, self.d, positions, rotary.cos, rotary.sin, k_cache, v_cache,
+                                meta.slot_mapping)
         q = qkv[:, :hd].view(t, self.h, self.d)
         k = qkv[:, hd:hd + kvd].view(t, self.kv, self.d)
         v = qkv[:, hd + kvd:].view(t, self.kv, self.d)
-        o = self.backend.forward(q, k, v, k_cache, v_cache, meta, self.scale)
+        o = self.backend.forward(q, k, v, k_cache, v_cache, meta, self.scale, kv_written=True)
         return self.o_proj(o.view(t, hd))
 
 

@@ -150,6 +150,31 @@ def test_prefill_and_write_kv_argument_checks():
     assert lib.nimbus_write_kv(*wk) == _lib.NIMBUS_ERR_UNSUPPORTED
 
 
+def test_rope_write_kv_rejects_before_launch():
+    """Every argument the fused rotary + slot write refuses returns its code
+    before any pointer is touched."""
+    lib = _lib.load()
+
+    def call(**kw):
+        a = dict(qkv=DUMMY, qs=48 * 128, t=5, h=32, kv=8, d=128, pos=DUMMY, cos=DUMMY, sin=DUMMY, ts=128, mp=4096,
+                 kc=DUMMY, vc=DUMMY, slots=DUMMY, ns=1600, dt=1)
+        a.update(kw)
+        return lib.nimbus_rope_write_kv(a["qkv"], a["qs"], a["t"], a["h"], a["kv"], a["d"], a["pos"], a["cos"],
+                                        a["sin"], a["ts"], a["mp"], a["kc"], a["vc"], a["slots"], a["ns"], a["dt"],
+                                        None)
+
+    assert call(t=0) == 0  # no tokens: nothing to launch
+    assert call(d=72) == _lib.NIMBUS_ERR_UNSUPPORTED  # head_dim % 16
+    assert call(dt=4) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert call(kv=0) == _lib.NIMBUS_ERR_INVALID
+    assert call(slots=None) == _lib.NIMBUS_ERR_INVALID
+    assert call(qs=40 * 128) == _lib.NIMBUS_ERR_INVALID  # row narrower than q + k + v heads
+    assert call(ts=64) == _lib.NIMBUS_ERR_INVALID  # table row narrower than head_dim
+    assert call(kc=DUMMY + 8) == _lib.NIMBUS_ERR_ALIGNMENT
+    assert call(qs=48 * 128 + 4) == _lib.NIMBUS_ERR_ALIGNMENT
+    assert call(ts=130) == _lib.NIMBUS_ERR_ALIGNMENT
+
+
 def test_rms_norm_rejects_before_launch():
     """Shapes outside the kernel and null pointers return an error code; no
     pointer is dereferenced on the host, so null is safe to pass here."""

@@ -25,6 +25,7 @@ import torch
 import torch.nn.functional as F
 
 from nimbus_amd.graphs import DecodeGraphs
+from nimbus_amd.kernels import cache_ops
 from nimbus_amd.kernels.elementwise import greedy_step, rope_, silu_mul
 from nimbus_amd.model.attention import AttnMetadata
 from nimbus_amd.model.config import ModelConfig
@@ -201,6 +202,44 @@ def test_rope_kernel_is_the_reference_arithmetic(dtype, heads, d):
     keep[5] = False
     assert torch.equal(got[keep, :heads * d], want[keep])
     assert torch.equal(got[5], x[5]) and torch.equal(got[:, heads * d:], x[:, heads * d:])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("heads,kv,d,t", [(32, 8, 128, 301), (32, 4, 64, 37), (8, 8, 64, 1), (32, 8, 128, 2108)])
+def test_rope_write_kv_is_rope_then_write_kv(dtype, heads, kv, d, t):
+    """The fused launch leaves qkv and both caches exactly as rope_ on the q
+    and k heads followed by write_kv of the k and v heads do, including a
+    position past the table (its k goes to the cache unrotated) and slots
+    outside the cache (skipped)."""
+    announce(f"rope_write_kv {dtype} heads={heads} kv={kv} d={d} t={t}")
+    g = torch.Generator(device="cuda").manual_seed(d + t)
+    width = (heads + 2 * kv) * d
+    qkv = torch.randn(t, width + 8, generator=g, device="cuda").to(dtype)  # rows wider than the heads
+    pos = torch.randint(0, 500, (t,), generator=g, device="cuda")
+    blocks = (t + 40) // 16 + 1
+    slots = torch.randperm(blocks * 16, generator=g, device="cuda")[:t].contiguous()
+    if t > 5:
+        pos[3] = 700  # past the table
+        slots[4] = -1  # outside the cache
+        slots[5] = blocks * 16
+    ang = torch.arange(512, device="cuda", dtype=torch.float32)[:, None] * torch.rand(d // 2, generator=g,
+                                                                                      device="cuda")[None]
+    ang = torch.cat([ang, ang], -1)
+    cos, sin = ang.cos().contiguous(), ang.sin().contiguous()
+    kc0 = torch.randn(blocks, 16, kv, d, generator=g, device="cuda").to(dtype)
+    vc0 = torch.randn(blocks, 16, kv, d, generator=g, device="cuda").to(dtype)
+
+    want_qkv = rope_(qkv.clone(), heads + kv, d, pos, cos, sin)
+    want_k, want_v = kc0.clone(), vc0.clone()
+    hd, kvd = heads * d, kv * d
+    cache_ops.write_kv(want_qkv[:, hd:hd + kvd].view(t, kv, d), want_qkv[:, hd + kvd:width].view(t, kv, d),
+                       want_k, want_v, slots)
+
+    got_qkv, got_k, got_v = qkv.clone(), kc0.clone(), vc0.clone()
+    cache_ops.rope_write_kv(got_qkv, heads, kv, d, pos, cos, sin, got_k, got_v, slots)
+    torch.cuda.synchronize()
+    assert torch.equal(got_qkv, want_qkv)
+    assert torch.equal(got_k, want_k) and torch.equal(got_v, want_v)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
