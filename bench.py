@@ -687,13 +687,16 @@ def time_decode_step(steps, warmup, chain=16):
     per step, and greedy_chain (step graph + on-device token pick, no host
     round trip); then the same with the decoder projections quantized to
     INT8. Bytes per step: every weight once (int8 projections after
-    quantization) + every layer's visible K/V rows + the new K/V rows."""
+    quantization) + every layer's visible K/V rows + the new K/V rows.
+    Each run also replays the target's whole verification pass for the
+    same 64 sequences (VerifyGraphs, k = 4 drafts: 5 query tokens per
+    sequence, 320 in all)."""
     import random
 
     import torch
 
     from nimbus_amd import workloads
-    from nimbus_amd.graphs import DecodeGraphs
+    from nimbus_amd.graphs import DecodeGraphs, VerifyGraphs
     from nimbus_amd.model.config import LLAMA3_8B as cfg
     from nimbus_amd.model.llama import build_model
     from nimbus_amd.quant import quantize_model, weight_bytes
@@ -742,10 +745,19 @@ def time_decode_step(steps, warmup, chain=16):
         chain_ms = (time.perf_counter() - t0) * 1e3 / chain
         nbytes = wb + kv_bytes + 64 * cfg.num_layers * 2 * cfg.num_kv_heads * cfg.head_dim * 2
         del graphs
+        verify = VerifyGraphs(model, caches, bs, max_len, 64, 4, need + 64, "cuda")
+        verify.capture()
+        for _ in range(warmup):
+            verify.run(seqs)
+        verify_ms = statistics.mean(event_times_us(lambda i: verify.run(seqs), n,
+                                                   torch.cuda.current_stream())) / 1e3
+        del verify
         return {"weights": label, "weight_bytes": wb, "bytes_per_step": nbytes, "eager_ms": eager_ms,
                 "graph_replay_ms": replay_ms, "greedy_chain_ms_per_step": chain_ms,
                 "tokens_per_s": 64 / (chain_ms * 1e-3), "GBps": nbytes / (chain_ms * 1e-3) / 1e9,
-                "frac_hbm_peak": nbytes / (chain_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                "frac_hbm_peak": nbytes / (chain_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                "verify_pass_ms": verify_ms, "verify_query_tokens": 64 * 5,
+                "verify_query_tokens_per_s": 64 * 5 / (verify_ms * 1e-3)}
 
     res = {"workload": "Llama-3-8B shape (random weights), 64 decode sequences of BASELINE config 3 "
                        f"(sum ctx {sum(ctx)}), chains of {chain} greedy steps",

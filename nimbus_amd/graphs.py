@@ -28,6 +28,8 @@ VerifyAttentionGraphs does the same for speculative verification
 (nimbus/spec/engine.py:60-150): there every sequence feeds k + 1 tokens, all
 through the prefill call, which runs them in its verify form (the page-split
 decode kernels with k + 1 query columns per head) when they fit it.
+VerifyGraphs replays the target model's whole verification pass the same
+way, as the reference's VerifyGraphs does.
 """
 
 from __future__ import annotations
@@ -420,3 +422,152 @@ class DecodeGraphs:
         self.active[:n].fill_(1)
         self.active[n:b].fill_(0)
         return b
+
+
+class VerifyGraphs:
+    """The target model's whole verification pass replayed from hipGraphs.
+
+    Follows Nimbus's VerifyGraphs (nimbus/spec/engine.py:60-150): every
+    sequence feeds its last q = k + 1 <= block_size tokens (the pending token
+    and k drafts) through one forward pass of `model` (embedding, every
+    layer, final norm, logits), all as prefill tokens, so a step differs from
+    the captured one only in device data. One graph per batch size (1, 2, 4,
+    8, 16 below max_batch, then max_batch); padding sequences sit at
+    positions 0..q - 1 of the scratch block with context q. The tile table
+    is fixed at capture (one entry per sequence, q < 64 query rows) and the
+    host lists are placeholders the kernels never read.
+
+    kernel: "auto" lets the prefill call take its verify form (the page-split
+    decode kernels with q query columns per head) when the heads fit it;
+    "tile" pins the tile kernel, as in the reference. The graphs own a
+    workspace sized for max_batch and max_model_len, which the model's
+    backend holds while they are captured (and is restored afterwards).
+    """
+
+    def __init__(self, model, kv_layers, block_size: int, max_model_len: int, max_batch: int, k: int,
+                 scratch_block: int, device, kernel: str = "auto"):
+        if kernel not in ("auto", "tile"):
+            raise ValueError(f"kernel must be 'auto' or 'tile', got {kernel!r}")
+        if not 0 < k + 1 <= block_size:
+            raise ValueError(f"k + 1 = {k + 1} must fit one block of {block_size}")
+        self.model = model
+        self.kv_layers = kv_layers
+        self.block_size = block_size
+        self.q_len = q = k + 1
+        self.max_batch = max_batch
+        self.scratch_block = scratch_block
+        self.kernel = kernel
+        self.device = device
+        self.sizes = [b for b in VERIFY_SIZES if b < max_batch] + [max_batch]
+        width = -(-max_model_len // block_size)
+        i64, i32 = torch.int64, torch.int32
+        self.input_ids = torch.zeros(max_batch * q, dtype=i64, device=device)
+        self.positions = torch.zeros(max_batch * q, dtype=i64, device=device)
+        self.slots = torch.zeros(max_batch * q, dtype=i64, device=device)
+        self.ctx = torch.full((max_batch,), q, dtype=i32, device=device)
+        self.tables = torch.full((max_batch, width), scratch_block, dtype=i32, device=device)
+        self.qstart = torch.arange(0, (max_batch + 1) * q, q, dtype=i32, device=device)
+        self._host = torch.empty((3, max_batch * q), dtype=i64, pin_memory=True)
+        self._host_ctx = torch.empty(max_batch, dtype=i32, pin_memory=True)
+        self._host_tables = torch.empty((max_batch, width), dtype=i32, pin_memory=True)
+        self._staged = None  # event after the last staged copies: the pinned rows are reused only after it
+        cfg = model.cfg
+        self.workspace = None
+        if kernel == "auto" and verify_queries(list(range(0, (max_batch + 1) * q, q)), cfg.num_heads,
+                                               cfg.num_kv_heads):
+            need = verify_workspace_bytes(max_batch, q, cfg.num_heads, cfg.head_dim, width * PAGE)
+            self.workspace = new_decode_workspace(need, device)
+        self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata]] = {}
+
+    def _meta(self, b: int) -> AttnMetadata:
+        empty = torch.zeros(0, dtype=torch.int32, device=self.device)
+        q = self.q_len
+        progs = (torch.arange(b, dtype=torch.int32, device=self.device),
+                 torch.zeros(b, dtype=torch.int32, device=self.device))
+        return AttnMetadata(
+            slot_mapping=self.slots[:b * q], num_prefill_tokens=b * q,
+            prefill_query_start=self.qstart[:b + 1], prefill_context_lens=self.ctx[:b],
+            prefill_block_tables=self.tables[:b],
+            decode_context_lens=empty, decode_block_tables=empty.view(0, 1), max_decode_context=0,
+            prefill_query_start_host=list(range(0, (b + 1) * q, q)), prefill_context_lens_host=[q] * b,
+            prefill_programs=progs, prefill_kernel=None if self.kernel == "auto" else self.kernel,
+        )
+
+    def _step(self, b: int, meta: AttnMetadata) -> torch.Tensor:
+        n = b * self.q_len
+        return self.model.logits(self.model(self.input_ids[:n], self.positions[:n], self.kv_layers, meta))
+
+    @torch.inference_mode()
+    def capture(self) -> None:
+        backend = self.model.backend
+        held = backend.decode_workspace
+        if self.workspace is not None:
+            backend.decode_workspace = self.workspace
+        try:
+            pool = torch.cuda.graph_pool_handle()
+            for b in reversed(self.sizes):
+                self._load([], b)  # valid padding everywhere before the warm-up passes
+                meta = self._meta(b)
+                for _ in range(2):
+                    self._step(b, meta)
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=pool):
+                    logits = self._step(b, meta)
+                self.graphs[b] = (g, logits, meta)  # meta's tensors (the tile table) must outlive the graph
+            torch.cuda.synchronize()
+        finally:
+            backend.decode_workspace = held
+
+    def padded_size(self, n: int) -> int:
+        return self.sizes[bisect.bisect_left(self.sizes, n)]
+
+    def _load(self, seqs, b: int) -> None:
+        """Stages the last q tokens of every sequence (token, position, the
+        slot table[p // bs] * bs + p % bs, context len(s), the block table)
+        and the padding rows (token 0 at positions 0..q - 1 of the scratch
+        block, context q) in pinned host memory, then copies each buffer in
+        one go (the contract of nimbus/spec/engine.py:114-139)."""
+        q, bs, n = self.q_len, self.block_size, len(seqs)
+        if self._staged is not None:
+            self._staged.synchronize()  # the previous call's copies have read the pinned rows
+        rows, ctx, tables = self._host.numpy(), self._host_ctx.numpy(), self._host_tables.numpy()
+        tables[:b] = 0
+        for i, s in enumerate(seqs):
+            if len(s) < q:
+                raise ValueError(f"sequence {i} holds {len(s)} tokens, fewer than the {q} it must feed")
+            if len(s.block_table) > tables.shape[1]:
+                raise ValueError("a block table is wider than max_model_len allows")
+            tables[i, :len(s.block_table)] = s.block_table
+            ctx[i] = len(s)
+            rows[0, i * q:(i + 1) * q] = s.token_ids[len(s) - q:]
+        pos = (ctx[:n, None].astype(np.int64) - q + np.arange(q)[None, :]).reshape(-1)
+        rows[1, :n * q] = pos
+        rows[2, :n * q] = tables[np.repeat(np.arange(n), q), pos // bs].astype(np.int64) * bs + pos % bs
+        pad = np.arange(q, dtype=np.int64)
+        rows[0, n * q:b * q] = 0
+        rows[1, n * q:b * q] = np.tile(pad, b - n)
+        rows[2, n * q:b * q] = np.tile(self.scratch_block * bs + pad, b - n)
+        ctx[n:b] = q
+        tables[n:b, 0] = self.scratch_block
+        for dst, src in ((self.input_ids, self._host[0]), (self.positions, self._host[1]),
+                         (self.slots, self._host[2])):
+            dst[:b * q].copy_(src[:b * q], non_blocking=True)
+        self.ctx[:b].copy_(self._host_ctx[:b], non_blocking=True)
+        self.tables[:b].copy_(self._host_tables[:b], non_blocking=True)
+        self._staged = torch.cuda.Event()
+        self._staged.record()
+
+    @torch.inference_mode()
+    def run(self, seqs) -> torch.Tensor:
+        """The verification pass for seqs (each feeding its last q tokens);
+        returns their logits [len(seqs) * q, vocab] (fp32, a view of the
+        graph's output, valid until the next replay)."""
+        n = len(seqs)
+        if not 0 < n <= self.max_batch:
+            raise ValueError(f"batch {n} outside 1..{self.max_batch}")
+        b = self.padded_size(n)
+        self._load(seqs, b)
+        g, logits, _ = self.graphs[b]
+        g.replay()
+        return logits[:n * self.q_len]

@@ -24,7 +24,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from nimbus_amd.graphs import DecodeGraphs
+from nimbus_amd.graphs import DecodeGraphs, VerifyGraphs
 from nimbus_amd.kernels import cache_ops
 from nimbus_amd.kernels.elementwise import greedy_step, rope_, silu_mul
 from nimbus_amd.model.attention import AttnMetadata
@@ -126,6 +126,50 @@ def test_decode_graphs_match_eager(n, dtype):
             s.feed(t)
         for s, t in zip(e_seqs, e_tok):
             s.feed(t)
+
+
+@pytest.mark.parametrize("n,dtype,kernel", [(3, torch.float16, "auto"), (5, torch.bfloat16, "auto"),
+                                             (8, torch.float16, "tile")])
+def test_verify_graphs_match_eager(n, dtype, kernel):
+    """The whole-model verification graph (nimbus/spec/engine.py:60-150):
+    every sequence feeds its pending token and k drafts; the replayed logits
+    of all k + 1 rows equal an eager forward pass over the same tokens within
+    rounding, with the same argmax, over three rounds in which a prefix of
+    the drafts is kept and the rest overwritten."""
+    announce(f"verify graphs n={n} {dtype} {kernel}")
+    k = 4
+    q = k + 1
+    model, caches, seqs = _setup(dtype, [3 + 9 * i for i in range(n)], num_blocks=160, seed=20 + n)
+    _prefill(model, caches, seqs)
+    g_seqs, e_seqs = _clone_seqs(seqs), _clone_seqs(seqs)
+    g_caches, e_caches = _clone_caches(caches), _clone_caches(caches)
+    graphs = VerifyGraphs(model, g_caches, BS, max_model_len=512, max_batch=8, k=k, scratch_block=160,
+                          device="cuda", kernel=kernel)
+    graphs.capture()
+    rng = random.Random(n)
+    for round_i in range(3):
+        drafts = [[rng.randrange(1, CFG.vocab_size) for _ in range(k)] for _ in range(n)]
+        for ss in (g_seqs, e_seqs):
+            for s, d in zip(ss, drafts):
+                s.token_ids.extend(d)
+        got = graphs.run(g_seqs).clone()
+        step = flat_step([(s, q) for s in e_seqs], "cuda", BS)
+        want = model.logits(model(step.input_ids, step.positions, e_caches, step.meta))
+        assert got.shape == want.shape == (n * q, CFG.vocab_size)
+        torch.testing.assert_close(got, want, atol=1e-2, rtol=1e-2)
+        g_tok, e_tok = got.argmax(-1).view(n, q).tolist(), want.argmax(-1).view(n, q).tolist()
+        assert g_tok == e_tok, round_i
+        # keep a prefix of each sequence's drafts, then the target's token after it
+        for i in range(n):
+            keep = rng.randrange(0, k + 1)
+            for ss in (g_seqs, e_seqs):
+                s = ss[i]
+                del s.token_ids[len(s) - k + keep:]
+                s.num_computed = len(s)
+                s.token_ids.append(g_tok[i][keep])
+    for (ka, va), (kb, vb) in zip(g_caches, e_caches):
+        torch.testing.assert_close(ka[:160], kb[:160], atol=1e-2, rtol=1e-2)
+        torch.testing.assert_close(va[:160], vb[:160], atol=1e-2, rtol=1e-2)
 
 
 def test_greedy_chain_matches_stepwise_runs():
