@@ -82,20 +82,19 @@ __device__ __forceinline__ u32x4 i8x8_to_operand<kFloat16>(uint32_t w0, uint32_t
   return u32x4{a[0], a[1], b[0], b[1]};
 }
 
-// bf16: byte b + 128 goes under the fp32 exponent of 2^23 and 2^23 + 128 is
-// subtracted (exact); the upper half of that fp32 is b's bf16, exactly.
+// bf16: each byte, sign-extended, converts to fp32 exactly (one
+// v_cvt_f32_i32 whose SDWA operand select picks and extends the byte), and
+// the upper half of that fp32 is the byte's bf16, exactly (|b| <= 128 needs
+// at most 8 significant bits). Six VALU ops per four weights.
 __device__ __forceinline__ u32x2 i8x4_to_bf16x4(uint32_t w) {
-  const uint32_t u = w ^ 0x80808080u;
-  float f[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // bytes [u_i, 0, 0, 0x4B] of (src0 = 0x4B000000, src1 = u)
-    const uint32_t bits = __builtin_amdgcn_perm(0x4B000000u, u, 0x07060500u | static_cast<uint32_t>(i));
-    f[i] = __uint_as_float(bits) - 8388736.f;
-  }
+  const int32_t s = static_cast<int32_t>(w);
+  const float f0 = static_cast<float>((s << 24) >> 24);
+  const float f1 = static_cast<float>((s << 16) >> 24);
+  const float f2 = static_cast<float>((s << 8) >> 24);
+  const float f3 = static_cast<float>(s >> 24);
   // upper halves of (f0, f1) and (f2, f3)
-  return u32x2{__builtin_amdgcn_perm(__float_as_uint(f[1]), __float_as_uint(f[0]), 0x07060302u),
-               __builtin_amdgcn_perm(__float_as_uint(f[3]), __float_as_uint(f[2]), 0x07060302u)};
+  return u32x2{__builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u),
+               __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u)};
 }
 
 template <>
