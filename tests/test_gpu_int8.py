@@ -167,12 +167,59 @@ def test_every_launch_plan_is_exact(m, n, k):
     lib = _lib.load()
     plans = mod._candidate_plans(m, n, k)
     assert plans
+    # one workspace for every plan, each run twice into an output poisoned with NaN
+    need = max(lib.nimbus_int8_matmul_packed_plan_workspace_bytes(m, n, k, *plan) for plan in plans)
+    ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
     for plan in plans:
-        need = lib.nimbus_int8_matmul_packed_plan_workspace_bytes(m, n, k, *plan)
-        ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
-        y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+        for rep in range(2):
+            y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+            rc = lib.nimbus_int8_matmul_packed_plan(x.data_ptr(), k, p.data_ptr(), s.data_ptr(), y.data_ptr(), n, m, n,
+                                                    k, *plan, ws.data_ptr(), ws.numel(), 1, None)
+            assert rc == 0, plan
+            torch.cuda.synchronize()
+            assert torch.equal(y.cpu(), want), (plan, rep)
+
+
+def test_split_plan_replays_in_a_graph():
+    """A plan that splits K (its kernel and the reducing launch), captured in
+    a hipGraph and replayed several times with eager calls on the same
+    workspace in between: every replay and every eager call gives the exact
+    product."""
+    from nimbus_amd import _lib
+
+    announce("int8 split plan in a graph")
+    m, n, k = 64, 4096, 4096
+    plan = (64, 2, 4, 1)
+    g = torch.Generator(device="cuda").manual_seed(9)
+    x = torch.randint(-3, 4, (m, k), generator=g, device="cuda").to(torch.bfloat16)
+    q = torch.randint(-127, 128, (n, k), generator=g, device="cuda").to(torch.int8)
+    s = (2.0 ** -torch.randint(6, 10, (n,), generator=g, device="cuda").float()).to(torch.bfloat16)
+    want = torch.from_numpy(closed_form.int8_matmul(x.cpu(), q.cpu(), s.cpu())).to(torch.bfloat16).cuda()
+    p = pack_int8_weight(q)
+    lib = _lib.load()
+    need = lib.nimbus_int8_matmul_packed_plan_workspace_bytes(m, n, k, *plan)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    y = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device="cuda")
+
+    def call():
         rc = lib.nimbus_int8_matmul_packed_plan(x.data_ptr(), k, p.data_ptr(), s.data_ptr(), y.data_ptr(), n, m, n, k,
-                                                *plan, ws.data_ptr(), ws.numel(), 1, None)
-        assert rc == 0, plan
+                                                *plan, ws.data_ptr(), ws.numel(), 1,
+                                                torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+
+    call()
+    torch.cuda.synchronize()
+    assert torch.equal(y, want)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for rep in range(4):
+        y.fill_(float("nan"))
+        graph.replay()
         torch.cuda.synchronize()
-        assert torch.equal(y.cpu(), want), plan
+        assert torch.equal(y, want), rep
+        y.fill_(float("nan"))
+        call()
+        torch.cuda.synchronize()
+        assert torch.equal(y, want), rep
