@@ -121,8 +121,9 @@ def log(msg):
 
 
 TRAFFIC_RECORD = os.path.join(ROOT, "profiles", "decode_llama3_traffic.json")
-DECODE_SOURCES = ("nimbus_amd/csrc/paged_decode.hip", "nimbus_amd/csrc/common.h",
-                  "nimbus_amd/csrc/nimbus_attn_internal.h", "include/nimbus_attn.h")
+# The files the decode kernels' code comes from (the public header and the
+# internal one only add declarations and constants those kernels do not use).
+DECODE_SOURCES = ("nimbus_amd/csrc/paged_decode.hip", "nimbus_amd/csrc/common.h")
 
 
 def decode_source_hash():
