@@ -62,7 +62,7 @@ other_configs BASELINE configs 1, 2 and 5 in compact form (at most 50
 Between timed calls the K/V pool rotates over enough copies (>= 1.5 GB) that
 the 256 MB Infinity Cache cannot serve one call's pages to the next.
 
---all also times every BASELINE config and writes gpurun_out/bench_configs.json.
+--all also times every BASELINE config (--all-out PATH writes the full rows as JSON).
 """
 
 from __future__ import annotations
@@ -91,6 +91,7 @@ def parse(argv=None):
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--all", action="store_true", help="also time every BASELINE config")
+    ap.add_argument("--all-out", default=None, metavar="PATH", help="with --all: also write the full rows as JSON")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--decode-only", action="store_true",
@@ -873,7 +874,7 @@ def other_configs(steps, warmup, prefill=True):
 
 # ---------------------------------------------------------------- --all
 
-def all_configs(steps, warmup):
+def all_configs(steps, warmup, out_path=None):
     import torch
 
     from nimbus_amd import workloads
@@ -899,9 +900,9 @@ def all_configs(steps, warmup):
         rows[name] = r
         del b
         torch.cuda.empty_cache()
-    os.makedirs(os.path.join(ROOT, "gpurun_out"), exist_ok=True)
-    with open(os.path.join(ROOT, "gpurun_out", "bench_configs.json"), "w") as f:
-        json.dump(rows, f, indent=1)
+    if out_path:
+        with open(out_path, "w") as f:
+            json.dump(rows, f, indent=1)
     for k, v in rows.items():
         log(f"{k}: " + ", ".join(f"{a}={b:.4g}" if isinstance(b, float) else f"{a}={b}" for a, b in v.items()
                                  if not isinstance(b, dict)))
@@ -1012,7 +1013,7 @@ def main(argv=None):
         log(f"reference_shapes: {result['reference_shapes']}")
     if args.all:
         result["configs"] = {k: {a: b for a, b in v.items() if not isinstance(b, dict)}
-                             for k, v in all_configs(args.steps, args.warmup).items()}
+                             for k, v in all_configs(args.steps, args.warmup, args.all_out).items()}
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle on host cores)")
         base = cpu_decode_baseline(batch, args.cpu_seconds)
