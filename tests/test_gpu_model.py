@@ -31,7 +31,7 @@ from nimbus_amd.model.attention import AttnMetadata
 from nimbus_amd.model.config import ModelConfig
 from nimbus_amd.model.llama import build_model
 from nimbus_amd.quant import quantize_model
-from nimbus_amd.workloads import SeqState, flat_step
+from nimbus_amd.workloads import SeqState, flat_step, is_decode
 from oracle import model as omodel
 from tests.gpu_helpers import announce
 
@@ -103,6 +103,66 @@ def _clone_seqs(seqs):
 
 def _clone_caches(caches):
     return [(kc.clone(), vc.clone()) for kc, vc in caches]
+
+
+def test_interleaved_batches_match_solo_runs():
+    """The property of nimbus tests/test_paged.py:63-95 on the GPU path:
+    sequences whose prompts go through in random chunks while others
+    decode, on scattered blocks, produce their solo runs' results. Both runs
+    feed the solo run's tokens (the interleaved run is teacher-forced), and
+    every sampled logits row matches the solo row within rounding, with the
+    same argmax wherever the solo row's top two differ by more than 0.05 (the
+    batch moves decode's split points, so rows can differ in the last bits,
+    which the reference's fp32 CPU run does not)."""
+    announce("interleaved chunked batches vs solo runs")
+    model, caches, _ = _setup(torch.float16, [], num_blocks=200, seed=31)
+    rng = random.Random(1)
+    prompts = [[rng.randrange(1, CFG.vocab_size) for _ in range(rng.randrange(1, 40))] for _ in range(6)]
+    n_new = 12
+    solo = []
+    for p in prompts:
+        s = SeqState(list(p), list(range(-(-(len(p) + n_new) // BS))))
+        rows = []
+        _, lg = _eager_step(model, caches, [(s, len(s))])
+        for i in range(n_new):
+            rows.append(lg[0].clone())
+            s.feed(int(lg[0].argmax()))
+            if i + 1 < n_new:
+                _, lg = _eager_step(model, caches, [(s, 1)])
+        solo.append((list(s.token_ids), rows))
+
+    pool = rng.sample(range(200), 200)
+    seqs = [SeqState(list(p), [pool.pop() for _ in range(-(-(len(p) + n_new) // BS))]) for p in prompts]
+    got = [0] * len(seqs)
+    waiting, running = list(range(len(seqs))), []
+    checked = 0
+    while any(g < n_new for g in got):
+        for _ in range(2):
+            if waiting:
+                running.append(waiting.pop(0))
+        active = [i for i in running if got[i] < n_new]
+        pre = [i for i in active if not is_decode(seqs[i], len(seqs[i]) - seqs[i].num_computed)]
+        dec = [i for i in active if i not in pre]
+        batch = [(seqs[i], min(len(seqs[i]) - seqs[i].num_computed, rng.randrange(1, 12))) for i in pre]
+        batch += [(seqs[i], 1) for i in dec]
+        order = pre + dec
+        _, lg = _eager_step(model, caches, batch)
+        row = 0
+        for i, (s, n) in zip(order, batch):
+            s.num_computed += n
+            if s.num_computed < len(s):
+                continue
+            want = solo[i][1][got[i]]
+            torch.testing.assert_close(lg[row], want, atol=1e-2, rtol=1e-2)
+            top2 = want.topk(2).values
+            if float(top2[0] - top2[1]) > 0.05:
+                assert int(lg[row].argmax()) == int(want.argmax()), (i, got[i])
+            row += 1
+            checked += 1
+            s.token_ids.append(solo[i][0][len(s)])  # the solo run's next token
+            got[i] += 1
+        assert row == lg.shape[0]
+    assert checked == len(prompts) * n_new
 
 
 @pytest.mark.parametrize("n,dtype", [(5, torch.float16), (3, torch.bfloat16), (16, torch.float16)])

@@ -67,6 +67,43 @@ def test_group_sizes_dtypes_and_long_chunks(dtype, heads, kv, d):
     assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="vs oracle")
 
 
+@pytest.mark.parametrize("kernel", ["auto", "tile"])
+def test_zero_length_sequences_inside_a_batch(kernel):
+    """Sequences feeding no query (q_len 0, with or without a cached
+    context) between others: they get no tile, and the other sequences'
+    rows match the oracle (the reference's loop builds no program for them,
+    prefill_attention.py:81-90)."""
+    announce(f"prefill zero-length sequences kernel={kernel}")
+    seqs = [(5, 40), (0, 17), (64, 64), (0, 30), (3, 3), (0, 1)]
+    args = _case(32, 8, 128, seqs, torch.bfloat16, seed=6)
+    got = paged_prefill_attention(*args, kernel=kernel)
+    q, k, v, _, _, bt, scale, qs, ctx = args
+    assert got.shape == q.shape
+    assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx, bt, scale), what="vs oracle")
+
+
+def test_empty_batches_return_empty():
+    """A prefill with no sequences, one whose sequences all feed no query,
+    and a decode of zero sequences launch nothing and return empty outputs."""
+    from nimbus_amd.kernels.paged_attention import paged_decode_attention
+
+    announce("empty prefill and decode batches")
+    k, v = scattered_cache(8, 16, 8, 128, seed=1, dtype=torch.bfloat16, device="cuda")
+    q0 = torch.empty(0, 32, 128, dtype=torch.bfloat16, device="cuda")
+    none = torch.zeros(0, 1, dtype=torch.int32, device="cuda")
+    got = paged_prefill_attention(q0, k, v, torch.zeros(1, dtype=torch.int32, device="cuda"),
+                                  torch.zeros(0, dtype=torch.int32, device="cuda"), none, 0.1, [0], [])
+    assert got.shape == (0, 32, 128)
+    bt = random_tables([20, 9], 16, 8, seed=2, device="cuda")
+    got = paged_prefill_attention(q0, k, v, torch.zeros(3, dtype=torch.int32, device="cuda"),
+                                  torch.tensor([20, 9], dtype=torch.int32, device="cuda"), bt, 0.1, [0, 0, 0],
+                                  [20, 9])
+    assert got.shape == (0, 32, 128)
+    got = paged_decode_attention(q0, k, v, torch.zeros(0, dtype=torch.int32, device="cuda"), none, 4096, 0.1)
+    torch.cuda.synchronize()
+    assert got.shape == (0, 32, 128)
+
+
 def test_prebuilt_programs_and_out_slice():
     announce("prefill programs + out slice")
     seqs = [(70, 90), (5, 5)]
