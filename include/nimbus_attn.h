@@ -159,7 +159,10 @@ int nimbus_paged_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_str
  * (already written by nimbus_write_kv) through block_tables[i].
  * prog_seq/prog_m is the tile table of build_programs
  * (prefill_attention.py:81-90): one entry (sequence, first query offset) per
- * NIMBUS_PREFILL_TILE query positions; num_programs entries.
+ * NIMBUS_PREFILL_TILE query positions; num_programs entries. Cache strides
+ * must satisfy cache_stride_token <= 2^25 and cache_stride_block < 2^30
+ * elements (pages are addressed with 32-bit offsets); others return
+ * NIMBUS_ERR_UNSUPPORTED.
  */
 #define NIMBUS_PREFILL_TILE 64
 int nimbus_paged_prefill(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,

@@ -107,6 +107,15 @@ __device__ __forceinline__ int v_pos(int key, int c) {
   return c ^ ((2 * key) & (D / 8 - 1));
 }
 
+// min(max(x, 0), 16) on a wave-uniform x, in scalar instructions: written
+// plainly, the compiler forms the clamp as v_med3_i32 (a vector instruction)
+// and copies the result back with v_readfirstlane.
+__device__ __forceinline__ int scalar_clamp16(int x) {
+  int r;
+  asm("s_max_i32 %0, %1, 0\n\ts_min_i32 %0, %0, 16" : "=&s"(r) : "s"(x) : "scc");
+  return r;
+}
+
 __device__ __forceinline__ int32_t scalar_load_i32(const int32_t* p, int i) {
   typedef const __attribute__((address_space(4))) int32_t* const_ptr;
   return ((const_ptr)(p))[i];
@@ -225,7 +234,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   };
   const char* kbytes = reinterpret_cast<const char*>(a.kc + static_cast<int64_t>(kvh) * a.c_sh);
   const char* vbytes = reinterpret_cast<const char*>(a.vc + static_cast<int64_t>(kvh) * a.c_sh);
-  const int64_t page_bytes = a.c_sb * 2;
+  const uint32_t page_bytes = static_cast<uint32_t>(a.c_sb * 2);  // below 2^31 (host check)
   const int row_bytes = static_cast<int>(a.c_st * 2);
   const int lkey = tid / CPR;
   const int lc = tid % CPR;
@@ -246,11 +255,10 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     const int p0 = __builtin_amdgcn_readfirstlane(p.id[0]), p1 = __builtin_amdgcn_readfirstlane(p.id[1]);
     const int p2 = __builtin_amdgcn_readfirstlane(p.id[2]), p3 = __builtin_amdgcn_readfirstlane(p.id[3]);
     const int id = (j & 2) ? ((j & 1) ? p3 : p2) : ((j & 1) ? p1 : p0);
-    // (readfirstlane keeps the clamp, which has no scalar form, from making
-    // the resource look divergent)
-    const int rows = __builtin_amdgcn_readfirstlane(min(max(kv_end - 16 * (4 * blk + j), 0), 16));
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + id * page_bytes, 0, rows * row_bytes,
-                                             kBufferFlags);
+    const int rows = scalar_clamp16(kv_end - 16 * (4 * blk + j));
+    // ids are checked nonnegative: a 32 x 32 -> 64-bit product
+    const uint64_t off = static_cast<uint64_t>(static_cast<uint32_t>(id)) * page_bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base) + off, 0, rows * row_bytes, kBufferFlags);
   };
   typedef __attribute__((address_space(3))) void lds_void;
   auto dma_k = [&](const BlockPages& p, int blk, auto slot) {
@@ -649,6 +657,8 @@ static int prefill_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
   // Pages are read through buffer resources with 32-bit offsets: 16 token
   // rows of a page must span less than 2 GiB.
   if (cache_stride_token <= 0 || cache_stride_token > (int64_t{1} << 25)) return NIMBUS_ERR_UNSUPPORTED;
+  // A page's byte offset is formed as page id x page bytes, in 32 x 32 bits.
+  if (cache_stride_block <= 0 || cache_stride_block >= (int64_t{1} << 30)) return NIMBUS_ERR_UNSUPPORTED;
   if ((q_stride_t | q_stride_h | cache_stride_block | cache_stride_token | cache_stride_head | out_stride_t |
        out_stride_h) % 8 != 0)
     return NIMBUS_ERR_ALIGNMENT;

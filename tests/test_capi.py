@@ -143,7 +143,9 @@ def test_prefill_and_write_kv_argument_checks():
     assert lib.nimbus_paged_prefill(*base[:23], 8, *base[24:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # block size
     assert lib.nimbus_paged_prefill(*base[:16], 0, *base[17:]) == 0  # no tiles: nothing to launch
     assert lib.nimbus_paged_prefill(*base[:22], 80, *base[23:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # head dim
-    wk = [DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 0, 8, 128, 8 * 128, 128, 8 * 128, 128, 1600, 1, None]
+    # page offsets are 32 x 32-bit products: block strides of 2^30 elements and up are refused
+    assert lib.nimbus_paged_prefill(*base[:6], 1 << 30, *base[7:]) == _lib.NIMBUS_ERR_UNSUPPORTED
+    wk =[DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 0, 8, 128, 8 * 128, 128, 8 * 128, 128, 1600, 1, None]
     assert lib.nimbus_write_kv(*wk) == 0  # zero tokens
     wk[13] = 3
     wk[5] = 5
