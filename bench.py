@@ -172,6 +172,26 @@ def region_us(fn, steps, stream):
     return start.elapsed_time(end) * 1e3 / steps
 
 
+def warm_up(fn, calls, min_seconds=0.05):
+    """Runs fn(i) `calls` times, then keeps calling it until the GPU has been
+    busy with it for min_seconds: the clocks reach their steady state under a
+    heavy kernel only after some tens of milliseconds (an 8192-token prefill
+    runs 786 us per call in its first 10 calls and 508 us from the 50th on), so
+    a count of calls alone leaves long kernels timed on a cold chip."""
+    import torch
+
+    for i in range(calls):
+        fn(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    i = calls
+    while time.perf_counter() - t0 < min_seconds:
+        for _ in range(8):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def event_times_us(fn, steps, stream):
     """Runs fn(i) for i < steps with a HIP event pair around each call on
     `stream`; returns the per-call durations in microseconds."""
@@ -421,8 +441,7 @@ def time_prefill(batch, steps, warmup):
     def call(i):
         paged_prefill_attention(*args, progs, out=out)
 
-    for i in range(warmup):
-        call(i)
+    warm_up(call, warmup)
     us = region_us(call, steps, torch.cuda.current_stream())
     us_pairs = statistics.mean(event_times_us(call, steps, torch.cuda.current_stream()))
     seqs = batch.seqs[:batch.num_prefills]
