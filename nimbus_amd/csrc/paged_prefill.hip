@@ -423,8 +423,11 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     const BlockPages pg0 = load_pages(kbeg);
     issue_v(pg0, kbeg, IntC<0>{});
     dma_k(pg0, kbeg, IntC<0>{});
+    // K(kbeg + 1) goes with the first block's loads (slot 1 is free), so the
+    // first barrier waits for both at once. Past the context it reads zeros;
+    // past the piece it is never read.
+    dma_k(pg_v, kbeg + 1, IntC<1>{});
     __syncthreads();
-    dma_k(pg_v, kbeg + 1, IntC<1>{});  // past the context: zeros; past the piece: unused
     qk(IntC<0>{}, IntC<0>{}, sa);
     qk(IntC<0>{}, IntC<1>{}, sa);
     store_v(IntC<0>{});
