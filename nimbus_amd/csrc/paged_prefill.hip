@@ -94,17 +94,22 @@ struct PrefillOccupancy {
   static constexpr int kWavesPerEU = (GS == 1 && D == 128) ? 1 : 2;
 };
 
-// Swizzled 16-byte chunk positions of the LDS tiles. K rows are read sixteen
-// at a time (one key per lane column) by the QK operand loads; V rows sixteen
-// at a time by the transposed reads. XOR-ing the chunk index with a function
-// of the row spreads equal chunks of those rows over the LDS banks.
+// Swizzled 16-byte chunk positions of the LDS tiles. The 64 banks serve 256
+// bytes per cycle: sixteen lanes of a ds_read_b128, thirty-two of a
+// ds_read_b64_tr_b16. K rows are read sixteen at a time (one key per lane
+// column, all lanes the same chunk) by the QK operand loads; the transposed V
+// reads take eight rows and two adjacent chunks per 32 lanes. XOR-ing the
+// chunk index with a function of the row puts those reads on distinct banks.
+// At D = 128 a row is the 256 bytes; at D = 64 two rows share them (row parity
+// picks the half), so the function skips the parity bit: K uses key bits
+// 1-3, V bits 1-2 (chunk pairs).
 template <int D>
 __device__ __forceinline__ int k_pos(int key, int c) {
-  return c ^ (key & (D / 8 - 1));
+  return D == 128 ? c ^ (key & 15) : c ^ ((key >> 1) & 7);
 }
 template <int D>
 __device__ __forceinline__ int v_pos(int key, int c) {
-  return c ^ ((2 * key) & (D / 8 - 1));
+  return D == 128 ? c ^ ((2 * key) & 15) : c ^ (key & 6);
 }
 
 // min(max(x, 0), 16) on a wave-uniform x, in scalar instructions: written
