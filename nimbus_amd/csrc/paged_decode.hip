@@ -207,10 +207,12 @@ struct PageRef {
 // Swizzled position of 16-byte chunk c of V row r in LDS: rows are read
 // sixteen at a time by the transposed PV operand loads, and spreading equal
 // chunks of different rows over different banks keeps those reads
-// conflict-free up to the LDS bandwidth.
+// conflict-free up to the LDS bandwidth. At D = 64 two 128-byte rows share
+// the 256 bytes the 64 banks serve per cycle (row parity picks the half), so
+// the pattern uses row bits 1-2 there.
 template <int D>
 __device__ __forceinline__ int v_pos(int r, int c) {
-  return c ^ ((2 * r) & (D / 8 - 1));
+  return D == 128 ? c ^ ((2 * r) & 15) : c ^ (r & 6);
 }
 
 // STREAM: K/V pages are loaded nontemporally (streamed, not kept in the L2).
