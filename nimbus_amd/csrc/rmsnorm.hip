@@ -7,8 +7,9 @@
 //   y   = dtype(s * rsqrt(mean(s^2) + eps))   mean and scale in fp32
 //   out = dtype(w * y)               the weight multiply in the model dtype
 //
-// One 256-thread workgroup per row (four waves; a measured 1.1-1.4x over one
-// wave per row at 2k-4k columns). A lane owns 16-byte chunks of its row:
+// 256-thread workgroups (four waves; a measured 1.1-1.4x over one wave per row
+// at 2k-4k columns, and two waves per row measured 18% slower at 2108 x 4096)
+// that walk rows with the next row's loads in flight. A lane owns 16-byte chunks of its row:
 // every load and store of a wave is 1 KB contiguous. The row is read once (x,
 // and r when fused), the rounded sum stays in registers for the second pass,
 // and the sum of squares is reduced across each wave with lane shuffles and
@@ -67,84 +68,111 @@ __device__ __forceinline__ uint32_t pack_pair<kBFloat16>(f32x2 v) {
   return pack2(f32_to_bf16(v[0]), f32_to_bf16(v[1]));
 }
 
-// One workgroup of four waves per row. Lane l of wave wr owns the row's
-// 16-byte chunks c = l + 64 (wr + 4 i), i < NCH. All of a lane's loads (x, r
-// and the weight) are issued before anything is stored: the stores of the new
-// residual may alias the inputs as far as the compiler knows, so
-// interleaving them would serialise the row's round trips. The stores are
-// nontemporal (streamed past the L2; nothing here reads them again): 8.2 ->
-// 6.9 us at 2048 x 2048 fp16, unchanged at 2108 x 4096 bf16 and 64 rows.
+// Workgroups of four waves walk rows blockIdx.x, + gridDim.x, ... (one row
+// each when the grid covers the rows). Lane l of wave wr owns the row's
+// 16-byte chunks c = l + 64 (wr + 4 i), i < NCH; the weight is loaded once.
+// The next row's x and r are loaded before the current row's output is
+// stored, so a workgroup's reads and writes overlap. The new residual's
+// stores may alias the inputs as far as the compiler knows, so they stay
+// after the loads of the row they belong to (interleaving them would
+// serialise the round trips). Stores are nontemporal (streamed past the L2;
+// nothing here reads them again): 8.2 -> 6.9 us at 2048 x 2048 fp16,
+// unchanged at 2108 x 4096 bf16 and 64 rows.
 template <int DT, int NCH, bool RES>
 __global__ __launch_bounds__(256) void add_rms_norm_kernel(NormArgs a) {
-  const int row = blockIdx.x;
   const int wave = static_cast<int>(threadIdx.x) / 64;
   const int lane = threadIdx.x % 64;
   const int nchunk = a.cols / 8;
-  const uint16_t* xrow = a.x + static_cast<int64_t>(row) * a.sx;
-
-  u32x4 xw[NCH], rw[NCH], ww[NCH];
+  u32x4 ww[NCH], xw[NCH], rw[NCH];
+  bool on[NCH];
+  int cidx[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) {
-    const int idx = lane + 64 * (wave + 4 * c);
-    if (idx < nchunk) {
-      xw[c] = *reinterpret_cast<const u32x4*>(xrow + 8 * idx);
-      if constexpr (RES) rw[c] = *reinterpret_cast<const u32x4*>(a.r + static_cast<int64_t>(row) * a.sr + 8 * idx);
-      ww[c] = *reinterpret_cast<const u32x4*>(a.w + 8 * idx);
-    }
+    cidx[c] = lane + 64 * (wave + 4 * c);
+    on[c] = cidx[c] < nchunk;
+    if (on[c]) ww[c] = *reinterpret_cast<const u32x4*>(a.w + 8 * cidx[c]);
   }
-  f32x2 v[NCH][4];
-  float ss = 0.f;
+  auto load = [&](int row) {
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int idx = lane + 64 * (wave + 4 * c);
-    if (idx < nchunk) {
-      if constexpr (RES) {
-        u32x4 sw;
+    for (int c = 0; c < NCH; ++c) {
+      if (on[c]) {
+        xw[c] = *reinterpret_cast<const u32x4*>(a.x + static_cast<int64_t>(row) * a.sx + 8 * cidx[c]);
+        if constexpr (RES) rw[c] = *reinterpret_cast<const u32x4*>(a.r + static_cast<int64_t>(row) * a.sr + 8 * cidx[c]);
+      }
+    }
+  };
+  // Partial sums per wave, double-buffered: a wave that runs ahead writes the
+  // other half while the slowest still reads this row's (the next reuse of a
+  // half is two rows on, past the next row's barrier).
+  __shared__ float part[2][4];
+  int par = 0;
+  int row = blockIdx.x;
+  if (row < a.rows) load(row);
+  for (; row < a.rows; row += gridDim.x) {
+    f32x2 v[NCH][4];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      if (on[c]) {
+        if constexpr (RES) {
+          u32x4 sw;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            // The exact sum of two fp16 (or bf16) values fits fp32, so one
+            // rounding to the element type is the model dtype's own add.
+            sw[e] = pack_pair<DT>(unpack_pair<DT>(xw[c][e]) + unpack_pair<DT>(rw[c][e]));
+            v[c][e] = unpack_pair<DT>(sw[e]);
+          }
+          __builtin_nontemporal_store(
+              sw, reinterpret_cast<u32x4*>(a.rout + static_cast<int64_t>(row) * a.sro + 8 * cidx[c]));
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[c][e] = unpack_pair<DT>(xw[c][e]);
+        }
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          // The exact sum of two fp16 (or bf16) values fits fp32, so one
-          // rounding to the element type is the model dtype's own add.
-          sw[e] = pack_pair<DT>(unpack_pair<DT>(xw[c][e]) + unpack_pair<DT>(rw[c][e]));
-          v[c][e] = unpack_pair<DT>(sw[e]);
+          ss = __builtin_fmaf(v[c][e][0], v[c][e][0], ss);
+          ss = __builtin_fmaf(v[c][e][1], v[c][e][1], ss);
         }
-        __builtin_nontemporal_store(sw, reinterpret_cast<u32x4*>(a.rout + static_cast<int64_t>(row) * a.sro + 8 * idx));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[c][e] = unpack_pair<DT>(xw[c][e]);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        ss = __builtin_fmaf(v[c][e][0], v[c][e][0], ss);
-        ss = __builtin_fmaf(v[c][e][1], v[c][e][1], ss);
       }
     }
-  }
-  ss = wave_sum(ss);
-  __shared__ float part[4];
-  if (lane == 0) part[wave] = ss;
-  __syncthreads();
-  ss = (part[0] + part[1]) + (part[2] + part[3]);
-  const float inv = 1.f / __builtin_sqrtf(ss / static_cast<float>(a.cols) + a.eps);
+    const int next = row + static_cast<int>(gridDim.x);
+    if (next < a.rows) load(next);
+    ss = wave_sum(ss);
+    if (lane == 0) part[par][wave] = ss;
+    __syncthreads();
+    ss = (part[par][0] + part[par][1]) + (part[par][2] + part[par][3]);
+    par ^= 1;
+    const float inv = 1.f / __builtin_sqrtf(ss / static_cast<float>(a.cols) + a.eps);
 
-  uint16_t* orow = a.out + static_cast<int64_t>(row) * a.so;
+    uint16_t* orow = a.out + static_cast<int64_t>(row) * a.so;
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int idx = lane + 64 * (wave + 4 * c);
-    if (idx < nchunk) {
-      u32x4 ow;
+    for (int c = 0; c < NCH; ++c) {
+      if (on[c]) {
+        u32x4 ow;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f32x2 y = unpack_pair<DT>(pack_pair<DT>(v[c][e] * inv));  // dtype(s * rsqrt(...))
-        ow[e] = pack_pair<DT>(unpack_pair<DT>(ww[c][e]) * y);
+        for (int e = 0; e < 4; ++e) {
+          const f32x2 y = unpack_pair<DT>(pack_pair<DT>(v[c][e] * inv));  // dtype(s * rsqrt(...))
+          ow[e] = pack_pair<DT>(unpack_pair<DT>(ww[c][e]) * y);
+        }
+        __builtin_nontemporal_store(ow, reinterpret_cast<u32x4*>(orow + 8 * cidx[c]));
       }
-      __builtin_nontemporal_store(ow, reinterpret_cast<u32x4*>(orow + 8 * idx));
     }
   }
 }
 
+// Workgroups in flight: six per CU of a 256-CU part (the register budget
+// holds six four-wave workgroups per CU up to 4096 columns, four at 8192).
+// Measured against one workgroup per row (hipGraph of back-to-back calls,
+// alternated three times on one box): 2048 x 2048 fp16 6.50-6.55 us against
+// 6.86-6.92, 64 x 4096 bf16 4.08 against 4.35, 4096 x 4096 bf16 27.5-27.8
+// against 27.9-28.3, 2108 x 4096 bf16 16.9-17.4 against 17.2; grids of 512
+// to 1024 workgroups measured no better or slower.
+constexpr int kNormGrid = 1536;
+
 template <int DT, int NCH>
 static int launch_norm_nch(const NormArgs& a, hipStream_t s) {
-  const unsigned grid = static_cast<unsigned>(a.rows);
+  const unsigned grid = static_cast<unsigned>(a.rows < kNormGrid ? a.rows : kNormGrid);
   if (a.r) {
     hipLaunchKernelGGL((add_rms_norm_kernel<DT, NCH, true>), dim3(grid), dim3(256), 0, s, a);
   } else {
