@@ -301,7 +301,12 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
 
   // ---- per-wave math
   typedef f32x4 Scores[4][2];  // S^T of one block: [16-key block][16-row block]
-  float m_run[2] = {-INFINITY, -INFINITY};
+  // Running max before a row has seen a key: finite, so the rescale factor
+  // 2^(m_run - m_new) and the exponent s * scale_log2 - m_run need no -inf
+  // case (a masked score stays -inf; the first visible score always moves the
+  // max, before any P of its block is formed).
+  constexpr float kNoMax = -0x1p127f;
+  float m_run[2] = {kNoMax, kNoMax};
   f32x4 acc[ND][2];
   f32x4 lsum[2];  // row sums of the fp16 P, accumulated by MFMA (all four lanes' values equal)
 #pragma unroll
@@ -350,7 +355,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     float lm[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      float m = s[0][nb][0];
+      float m = -INFINITY;  // (a constant start spares the canonicalising max of the first score)
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb) {
 #pragma unroll
@@ -362,7 +367,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const float m_new = fmaxf(m_run[nb], max_across_groups(lm[nb]));
-        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m_run[nb] - m_new);
+        const float alpha = fast_exp2(m_run[nb] - m_new);
         m_run[nb] = m_new;
         lsum[nb] *= alpha;
 #pragma unroll
@@ -376,7 +381,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     constexpr int H = decltype(half)::value;
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      const float neg_m = m_run[nb] == -INFINITY ? 0.f : -m_run[nb];
+      const float neg_m = -m_run[nb];
       float p[2][4];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -516,7 +521,11 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
       float* po = a.part + row * D;
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd) *reinterpret_cast<f32x4*>(po + 16 * nd + 4 * grp) = acc[nd][nb];
-      if (grp == 0) *reinterpret_cast<float2*>(a.part + a.part_ml + row * 2) = make_float2(m_run[nb], lsum[nb][0]);
+      if (grp == 0) {
+        // a row that saw no key here: m = -inf, l = 0 (weighs nothing in the merge)
+        const float m_out = lsum[nb][0] == 0.f ? -INFINITY : m_run[nb];
+        *reinterpret_cast<float2*>(a.part + a.part_ml + row * 2) = make_float2(m_out, lsum[nb][0]);
+      }
     }
     return;
   }
