@@ -22,15 +22,16 @@
 // Per 64-key block the workgroup stages K and V (fp16; bf16 V converted)
 // into LDS, double-buffered, with XOR-swizzled 16-byte chunks; the next
 // block's global loads are in flight while the current one is computed.
-// Each wave then computes, for its 32 rows:
-//   S^T[key][row] = K[key][:] . Q^T[:][row]   16x16x32 MFMA, K read from LDS
+// Each wave then computes, for its 32 rows (lane l: row l % 32, lanes l and
+// l + 32 holding different keys of it):
+//   S^T[key][row] = K[key][:] . Q^T[:][row]   32x32x16 MFMA, K read from LDS
 //                                              in the A-operand layout, Q^T in
 //                                              registers
 //   softmax in the exp2 domain with a lazily raised running max: the max
 //   only moves when a score exceeds it by more than 2^8, so the rescale of
 //   O is rare and P = 2^(s - m) stays below 256 (exact range in fp16); row
 //   sums stay per lane until the end
-//   O^T[d][row]  += V^T[d][key] . P^T[key][row]  16x16x32 fp16 MFMA, V^T read
+//   O^T[d][row]  += V^T[d][key] . P^T[key][row]  32x32x16 fp16 MFMA, V^T read
 //                                              with ds_read_b64_tr_b16, P^T is
 //                                              the QK output layout as is
 // Causal and context masks are applied only on blocks that need them.
@@ -109,7 +110,7 @@ __device__ __forceinline__ int k_pos(int key, int c) {
 }
 template <int D>
 __device__ __forceinline__ int v_pos(int key, int c) {
-  return D == 128 ? c ^ ((2 * key) & 15) : c ^ (key & 6);
+  return D == 128 ? c ^ ((4 * key) & 12) : c ^ (4 * ((key >> 1) & 1));
 }
 
 // min(max(x, 0), 16) on a wave-uniform x, in scalar instructions: written
@@ -131,6 +132,22 @@ struct BlockPages {
   int id[4];
 };
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// 32x32x16 MFMA: a, b carry 8 16-bit elements each. Lane l holds A[m = l % 32]
+// [k = 8 (l / 32) + t] and B[k = 8 (l / 32) + t][n = l % 32]; result element
+// i of lane l is D[m = 8 (i / 4) + 4 (l / 32) + i % 4][n = l % 32].
+template <int DT>
+__device__ __forceinline__ f32x16 mfma_32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == kFloat16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+}
+
 template <int N>
 using IntC = std::integral_constant<int, N>;
 template <bool B>
@@ -141,8 +158,8 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   using Shape = PrefillShape<GS>;
   constexpr int NT = Shape::kThreads;
   constexpr int POS = Shape::kPos;
-  constexpr int KK = D / 32;                // 16x16x32 steps over the head dim (QK)
-  constexpr int ND = D / 16;                // 16-row blocks of O^T
+  constexpr int KK = D / 16;                // 32x32x16 steps over the head dim (QK)
+  constexpr int ND = D / 32;                // 32-row blocks of O^T
   constexpr int CPR = D / 8;                // 16-byte chunks per K/V row
   constexpr int PPT = kBlockN * CPR / NT;   // 16-byte pieces per thread per tile
   constexpr int TILE = kBlockN * D;         // u16 elements of one tile
@@ -186,32 +203,27 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64) & (Shape::kWaves - 1);  // scalar, range known
   const int lane = tid % 64;
-  const int col = lane % 16;
-  const int grp = lane / 16;
+  const int col = lane % 32;  // this lane's row of the wave's 32
+  const int kg = lane / 32;   // which of each 16-long k range it holds (8 kg .. 8 kg + 7)
 
-  // This lane's two rows (one per 16-row N block).
-  int qpos[2], head[2];
-  bool row_ok[2];
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int r = 32 * wave + 16 * nb + col;
-    const int pos = r / GS;
-    row_ok[nb] = m0 + pos < q_len;
-    qpos[nb] = base_pos + m0 + pos;
-    head[nb] = kvh * a.G + gsub * GS + r % GS;
+  // This lane's row (lanes l and l + 32 share it).
+  int qpos, head;
+  {
+    const int r = 32 * wave + col;
+    qpos = base_pos + m0 + r / GS;
+    head = kvh * a.G + gsub * GS + r % GS;
   }
   // Smallest position among this wave's rows: blocks wholly at or below it
   // (and inside the context) need no mask.
   const int wave_lo = base_pos + m0 + (32 * wave) / GS;
 
   // Q^T as the B operand (rows past q_len load the last query row).
-  u32x4 qop[2][KK];
+  u32x4 qop[KK];
+  {
+    const int pos = min((32 * wave + col) / GS, q_len - 1 - m0);
+    const uint16_t* qrow = a.q + static_cast<int64_t>(qs + m0 + pos) * a.q_st + static_cast<int64_t>(head) * a.q_sh;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int pos = min((32 * wave + 16 * nb + col) / GS, q_len - 1 - m0);
-    const uint16_t* qrow = a.q + static_cast<int64_t>(qs + m0 + pos) * a.q_st + static_cast<int64_t>(head[nb]) * a.q_sh;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) qop[nb][kk] = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * grp);
+    for (int kk = 0; kk < KK; ++kk) qop[kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk + 8 * kg);
   }
 
   // ---- staging
@@ -300,38 +312,37 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   };
 
   // ---- per-wave math
-  typedef f32x4 Scores[4][2];  // S^T of one block: [16-key block][16-row block]
+  // S^T of one block, per 32-key half h: element i of lane l is key
+  // 32 h + 8 (i / 4) + 4 kg + i % 4 of the block, row col.
+  typedef f32x16 Scores[2];
   // Running max before a row has seen a key: finite, so the rescale factor
   // 2^(m_run - m_new) and the exponent s * scale_log2 - m_run need no -inf
   // case (a masked score stays -inf; the first visible score always moves the
-  // max, before any P of its block is formed).
+  // max, before any P of its block is formed). Lanes l and l + 32 keep the
+  // same value for their shared row.
   constexpr float kNoMax = -0x1p127f;
-  float m_run[2] = {kNoMax, kNoMax};
-  f32x4 acc[ND][2];
-  f32x4 lsum[2];  // row sums of the fp16 P, accumulated by MFMA (all four lanes' values equal)
+  float m_run = kNoMax;
+  f32x16 acc[ND];  // O^T: element i of lane l is d = 32 nd + 8 (i / 4) + 4 kg + i % 4, row col
+  float lsum = 0.f;  // this lane's share of its row's sum of the fp16 P (the keys it holds)
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    lsum[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int nd = 0; nd < ND; ++nd) {
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd) acc[nd][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < 16; ++i) acc[nd][i] = 0.f;
   }
-  const u32x4 ones = u32x4{0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u};  // fp16 1.0
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 ones2 = h2{static_cast<_Float16>(1.f), static_cast<_Float16>(1.f)};
 
   // S^T[key][row] = K[key][:] . Q^T[:][row] for keys 32 h .. 32 h + 31.
   auto qk = [&](auto slot, auto half, Scores& s) {
     constexpr int H = decltype(half)::value;
     const uint16_t* kt = ks + slot * TILE;
+    const int key = 32 * H + col;
 #pragma unroll
-    for (int mb = 2 * H; mb < 2 * H + 2; ++mb) {
-      s[mb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      s[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int key = 16 * mb + col;
+    for (int i = 0; i < 16; ++i) s[H][i] = 0.f;
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const u32x4 kop = *reinterpret_cast<const u32x4*>(kt + key * D + 8 * k_pos<D>(key, 4 * kk + grp));
-        s[mb][0] = mfma_16x16x32<DT>(kop, qop[0][kk], s[mb][0]);
-        s[mb][1] = mfma_16x16x32<DT>(kop, qop[1][kk], s[mb][1]);
-      }
+    for (int kk = 0; kk < KK; ++kk) {
+      const u32x4 kop = *reinterpret_cast<const u32x4*>(kt + key * D + 8 * k_pos<D>(key, 2 * kk + kg));
+      s[H] = mfma_32x32x16<DT>(kop, qop[kk], s[H]);
     }
   };
   // Mask (raw scores; only blocks that reach past a row's position or the
@@ -342,78 +353,76 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
     const int k0 = blk * kBlockN;
     const bool full = k0 + kBlockN - 1 <= wave_lo && k0 + kBlockN <= kv_end;
     if (!full) {
+      const int lim = min(qpos + 1, kv_end) - k0 - 4 * kg;  // key offsets below lim are visible
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int lim = min(qpos[nb] + 1, kv_end) - k0 - 4 * grp;  // key offsets below lim are visible
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-        for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) s[mb][nb][r] = 16 * mb + r < lim ? s[mb][nb][r] : -INFINITY;
-        }
+        for (int i = 0; i < 16; ++i) s[h][i] = 32 * h + 8 * (i / 4) + i % 4 < lim ? s[h][i] : -INFINITY;
       }
     }
-    float lm[2];
+    float m = -INFINITY;  // (a constant start spares the canonicalising max of the first score)
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      float m = -INFINITY;  // (a constant start spares the canonicalising max of the first score)
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) m = fmaxf(m, s[mb][nb][r]);
-      }
-      lm[nb] = m * a.scale_log2;  // the scale is positive: max commutes with it
+      for (int i = 0; i < 16; ++i) m = fmaxf(m, s[h][i]);
     }
-    if (__builtin_amdgcn_ballot_w64(lm[0] > m_run[0] + kLazyMax || lm[1] > m_run[1] + kLazyMax) != 0) {
+    const float lm = m * a.scale_log2;  // the scale is positive: max commutes with it
+    if (__builtin_amdgcn_ballot_w64(lm > m_run + kLazyMax) != 0) {
+      const float m_new = fmaxf(m_run, fmaxf(lm, __shfl_xor(lm, 32, 64)));
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      lsum *= alpha;
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const float m_new = fmaxf(m_run[nb], max_across_groups(lm[nb]));
-        const float alpha = fast_exp2(m_run[nb] - m_new);
-        m_run[nb] = m_new;
-        lsum[nb] *= alpha;
-#pragma unroll
-        for (int nd = 0; nd < ND; ++nd) acc[nd][nb] *= alpha;
-      }
+      for (int nd = 0; nd < ND; ++nd) acc[nd] *= alpha;
     }
   };
-  // P^T = 2^(S^T * scale_log2 - m) for keys 32 h .. 32 h + 31 as fp16 B
-  // operands; a row with no score yet gives P = 0.
+  // P^T = 2^(S^T * scale_log2 - m) for keys 32 h .. 32 h + 31 as the fp16 B
+  // operands of the two P.V MFMAs (keys 32 h + 16 j ..); a row with no score
+  // yet gives P = 0. Operand element t (k = 8 kg + t) is S element 8 j + t,
+  // key 32 h + 16 j + 8 (t / 4) + 4 kg + t % 4.
   auto probs = [&](const Scores& s, auto half, u32x4 (&pop)[2]) {
     constexpr int H = decltype(half)::value;
+    const float neg_m = -m_run;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const float neg_m = -m_run[nb];
-      float p[2][4];
+    for (int j = 0; j < 2; ++j) {
+      float p[8];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) p[j][r] = fast_exp2(__builtin_fmaf(s[2 * H + j][nb][r], a.scale_log2, neg_m));
-      }
-      pop[nb] = u32x4{pack_f16_rtz(p[0][0], p[0][1]), pack_f16_rtz(p[0][2], p[0][3]), pack_f16_rtz(p[1][0], p[1][1]),
-                      pack_f16_rtz(p[1][2], p[1][3])};
+      for (int t = 0; t < 8; ++t) p[t] = fast_exp2(__builtin_fmaf(s[H][8 * j + t], a.scale_log2, neg_m));
+      pop[j] = u32x4{pack_f16_rtz(p[0], p[1]), pack_f16_rtz(p[2], p[3]), pack_f16_rtz(p[4], p[5]),
+                     pack_f16_rtz(p[6], p[7])};
     }
   };
-  // Transposed-read addresses (see lds_read_tr16): lane j of group grp reads
-  // V row 16 mb + 4 grp + j/4, elements 16 nd + 4 (j%4) .. +4.
-  const int tr_row = 4 * grp + col / 4;
-  const int tr_half = 4 * ((col % 4) % 2);
-  const int tr_chunk = (col % 4) / 2;
-  // O^T[d][row] += V^T[d][key] P^T[key][row]; row sums += 1^T P^T; keys
-  // 32 h .. 32 h + 31.
+  // Transposed-read addresses (see lds_read_tr16): in each 16-lane group
+  // (kg = group / 2, column half group % 2), lane i reads V row
+  // 32 h + 16 j + 4 kg + i / 4 (and + 8), elements
+  // 32 nd + 16 (group % 2) + 4 (i % 4) .. +4; lane i of the group then holds
+  // d = 32 nd + 16 (group % 2) + i, the A operand's row l % 32.
+  const int gi = lane % 16;
+  const int tr_row = 4 * kg + gi / 4;
+  const int tr_chunk = 2 * ((lane / 16) % 2) + (gi % 4) / 2;
+  const int tr_half = 4 * ((gi % 4) % 2);
+  // O^T[d][row] += V^T[d][key] P^T[key][row] for keys 32 h .. 32 h + 31; the
+  // lane's row-sum share += its P.
   auto pv = [&](auto slot, auto half, const u32x4 (&pop)[2]) {
     constexpr int H = decltype(half)::value;
     const uint16_t* vt = vs + slot * TILE;
-    const int r0 = 32 * H + tr_row;
-    const int r1 = r0 + 16;
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-      const u32x2 lo = lds_read_tr16(vt + r0 * D + 8 * v_pos<D>(r0, 2 * nd + tr_chunk) + tr_half);
-      const u32x2 hi = lds_read_tr16(vt + r1 * D + 8 * v_pos<D>(r1, 2 * nd + tr_chunk) + tr_half);
-      const u32x4 vop = u32x4{lo[0], lo[1], hi[0], hi[1]};
-      acc[nd][0] = mfma_16x16x32<kFloat16>(vop, pop[0], acc[nd][0]);
-      acc[nd][1] = mfma_16x16x32<kFloat16>(vop, pop[1], acc[nd][1]);
+    for (int j = 0; j < 2; ++j) {
+      const int r0 = 32 * H + 16 * j + tr_row;
+      const int r1 = r0 + 8;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+        const u32x2 lo = lds_read_tr16(vt + r0 * D + 8 * v_pos<D>(r0, 4 * nd + tr_chunk) + tr_half);
+        const u32x2 hi = lds_read_tr16(vt + r1 * D + 8 * v_pos<D>(r1, 4 * nd + tr_chunk) + tr_half);
+        const u32x4 vop = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        acc[nd] = mfma_32x32x16<kFloat16>(vop, pop[j], acc[nd]);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = pop[j][e];  // (a bit_cast of the vector subscript itself would read element 0)
+        lsum = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, w), ones2, lsum, false);
+      }
     }
-    lsum[0] = mfma_16x16x32<kFloat16>(ones, pop[0], lsum[0]);
-    lsum[1] = mfma_16x16x32<kFloat16>(ones, pop[1], lsum[1]);
   };
 
   // ---- the block pipeline
@@ -495,59 +504,58 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // reads any more); let them land before the workgroup's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
-  // The output rows' heads and bounds again, from a copy of the lane index
+  // The output row's head and bound again, from a copy of the lane index
   // the compiler cannot see through: keeping the prologue's values alive
   // across the walk would cost registers the walk needs.
   int lane_e = lane;
   asm volatile("" : "+v"(lane_e));
-  const int col_e = lane_e % 16;
-#pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    const int r = 32 * wave + 16 * nb + col_e;
-    row_ok[nb] = m0 + r / GS < q_len;
-    head[nb] = kvh * a.G + gsub * GS + r % GS;
-  }
+  const int col_e = lane_e % 32;
+  const int kg_e = lane_e / 32;
+  const int r_e = 32 * wave + col_e;
+  const bool row_ok = m0 + r_e / GS < q_len;
+  const int head_e = kvh * a.G + gsub * GS + r_e % GS;
+  const float l_row = lsum + __shfl_xor(lsum, 32, 64);  // both halves of the row's keys
 
   if (slot >= 0) {
     if (slot >= a.slots) return;
     // A piece: unnormalised O^T, the running max and the row sum, per row
-    // (rows past q_len are skipped; a row that saw no key here keeps
+    // (rows past q_len are skipped; a row that saw no key here writes
     // m = -inf, l = 0, O = 0 and weighs nothing in the merge).
+    if (!row_ok) return;
+    const int pos = m0 - m_entry + r_e / GS;
+    const int64_t row = (static_cast<int64_t>(slot) * kPrefillTile + pos) * a.H + head_e;
+    float* po = a.part + row * D;
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      if (!row_ok[nb]) continue;
-      const int pos = m0 - m_entry + (32 * wave + 16 * nb + col_e) / GS;
-      const int64_t row = (static_cast<int64_t>(slot) * kPrefillTile + pos) * a.H + head[nb];
-      float* po = a.part + row * D;
+    for (int nd = 0; nd < ND; ++nd) {
 #pragma unroll
-      for (int nd = 0; nd < ND; ++nd) *reinterpret_cast<f32x4*>(po + 16 * nd + 4 * grp) = acc[nd][nb];
-      if (grp == 0) {
-        // a row that saw no key here: m = -inf, l = 0 (weighs nothing in the merge)
-        const float m_out = lsum[nb][0] == 0.f ? -INFINITY : m_run[nb];
-        *reinterpret_cast<float2*>(a.part + a.part_ml + row * 2) = make_float2(m_out, lsum[nb][0]);
+      for (int q4 = 0; q4 < 4; ++q4) {
+        *reinterpret_cast<f32x4*>(po + 32 * nd + 8 * q4 + 4 * kg_e) =
+            f32x4{acc[nd][4 * q4], acc[nd][4 * q4 + 1], acc[nd][4 * q4 + 2], acc[nd][4 * q4 + 3]};
       }
+    }
+    if (kg_e == 0) {
+      const float m_out = l_row == 0.f ? -INFINITY : m_run;
+      *reinterpret_cast<float2*>(a.part + a.part_ml + row * 2) = make_float2(m_out, l_row);
     }
     return;
   }
 
+  if (!row_ok) return;
+  const float inv = 1.f / l_row;
+  const int pos = r_e / GS;
+  uint16_t* orow = a.out + static_cast<int64_t>(qs + m0 + pos) * a.o_st + static_cast<int64_t>(head_e) * a.o_sh;
 #pragma unroll
-  for (int nb = 0; nb < 2; ++nb) {
-    if (!row_ok[nb]) continue;
-    const float inv = 1.f / lsum[nb][0];
-    const int pos = (32 * wave + 16 * nb + col_e) / GS;
-    uint16_t* orow = a.out + static_cast<int64_t>(qs + m0 + pos) * a.o_st + static_cast<int64_t>(head[nb]) * a.o_sh;
+  for (int nd = 0; nd < ND; ++nd) {
 #pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-      const f32x4 o = acc[nd][nb];
-      const u32x2 w = u32x2{pack2(Elem<DT>::from_f32(o[0] * inv), Elem<DT>::from_f32(o[1] * inv)),
-                            pack2(Elem<DT>::from_f32(o[2] * inv), Elem<DT>::from_f32(o[3] * inv))};
-      *reinterpret_cast<u32x2*>(orow + 16 * nd + 4 * grp) = w;
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const f32x16& o = acc[nd];
+      const u32x2 w = u32x2{pack2(Elem<DT>::from_f32(o[4 * q4] * inv), Elem<DT>::from_f32(o[4 * q4 + 1] * inv)),
+                            pack2(Elem<DT>::from_f32(o[4 * q4 + 2] * inv), Elem<DT>::from_f32(o[4 * q4 + 3] * inv))};
+      *reinterpret_cast<u32x2*>(orow + 32 * nd + 8 * q4 + 4 * kg_e) = w;
     }
   }
 }
 
-// Combines the pieces of split tiles: one thread per (tile, position, head,
-// 8 elements of D). merges: [num_merges][4] = seq, m0, first slot, pieces.
 template <int DT, int D>
 __global__ __launch_bounds__(256) void paged_prefill_merge_kernel(PrefillArgs a, const int32_t* merges,
                                                                   int32_t num_merges) {
