@@ -132,6 +132,10 @@ struct BlockPages {
   int id[4];
 };
 
+// Key-block range and piece slot of a unit of the plain tile table: every
+// block of the unit, written as a whole (no piece).
+__constant__ int32_t kWholeUnit[3] = {0, INT32_MAX, -1};
+
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // 32x32x16 MFMA: a, b carry 8 16-bit elements each. Lane l holds A[m = l % 32]
@@ -176,23 +180,59 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   const int sub = r_unit % Shape::kSub;
   const int kvh = kvg_id / a.gsplit;
   const int gsub = kvg_id % a.gsplit;
-  int seq, m_entry, kb0 = 0, kb1 = INT32_MAX, slot = -1;
-  if (a.pieces) {
-    const int32_t* pe = a.pieces + 5 * entry;
-    seq = pe[0];
-    m_entry = pe[1];
-    kb0 = pe[2];
-    kb1 = pe[3];
-    slot = pe[4];
-  } else {
-    seq = a.prog_seq[entry];
-    m_entry = a.prog_m[entry];
-  }
+  // The unit's record (sequence, first query, key blocks [kb0, kb1), piece
+  // slot), read without a branch: the plain tile table takes its block range
+  // and slot from kWholeUnit. Before the first K/V copy the workgroup then
+  // waits on three dependent rounds of scalar loads: the kernel arguments,
+  // the record, and the sequence's bounds together with the page ids of its
+  // first three key blocks (indexed from kb0 and clamped to the table row, so
+  // they need no context length; a page past the context is read through an
+  // empty buffer resource, whatever id its table entry holds).
+  // (each empty asm below takes the values of one round, so the compiler
+  // issues that round's loads together and none of them later)
+  asm volatile("" ::"s"(a.pieces), "s"(a.prog_seq), "s"(a.prog_m), "s"(a.bt), "s"(a.bt_sb), "s"(a.qstart),
+               "s"(a.ctx), "s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.c_sb), "s"(a.c_st), "s"(a.c_sh));
+  const int32_t* p_rec = a.pieces ? a.pieces + 5 * entry : a.prog_seq + entry;
+  const int32_t* p_m = a.pieces ? p_rec + 1 : a.prog_m + entry;
+  const int32_t* p_blk = a.pieces ? p_rec + 2 : kWholeUnit;
+  int seq = scalar_load_i32(p_rec, 0);
+  int m_entry = scalar_load_i32(p_m, 0);
+  int kb0 = scalar_load_i32(p_blk, 0);
+  int kb1 = scalar_load_i32(p_blk, 1);
+  int slot = scalar_load_i32(p_blk, 2);
+  asm volatile("" : "+s"(seq), "+s"(m_entry), "+s"(kb0), "+s"(kb1), "+s"(slot));
+  const int32_t* btrow = a.bt + seq * a.bt_sb;
+  const int page_cap = a.bt_width - 1;
+  auto load_raw = [&](int blk) {
+    BlockPages p;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p.id[i] = scalar_load_i32(btrow, min(4 * blk + i, page_cap));
+    return p;
+  };
+  auto checked = [&](BlockPages p) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) p.id[i] = static_cast<uint32_t>(p.id[i]) < static_cast<uint32_t>(a.num_blocks) ? p.id[i] : 0;
+    return p;
+  };
+  auto load_pages = [&](int blk) { return checked(load_raw(blk)); };
+  int qs = scalar_load_i32(a.qstart, seq);
+  int qe = scalar_load_i32(a.qstart, seq + 1);
+  int ctx_in = scalar_load_i32(a.ctx, seq);
+  BlockPages pg_first = load_raw(kb0);
+  BlockPages pg_v = load_raw(kb0 + 1);  // pages of V(kb + 1)
+  BlockPages pg_k = load_raw(kb0 + 2);  // pages of K(kb + 2)
+  // (the compiler would otherwise sink these past the exit below, or check
+  // each page id as it lands and reuse its register: rounds of their own)
+  asm volatile("" : "+s"(qs), "+s"(qe), "+s"(ctx_in), "+s"(pg_first.id[0]), "+s"(pg_first.id[1]),
+               "+s"(pg_first.id[2]), "+s"(pg_first.id[3]), "+s"(pg_v.id[0]), "+s"(pg_v.id[1]), "+s"(pg_v.id[2]),
+               "+s"(pg_v.id[3]), "+s"(pg_k.id[0]), "+s"(pg_k.id[1]), "+s"(pg_k.id[2]), "+s"(pg_k.id[3]));
+  pg_first = checked(pg_first);
+  pg_v = checked(pg_v);
+  pg_k = checked(pg_k);
   const int m0 = m_entry + sub * POS;
-  const int qs = a.qstart[seq];
-  const int q_len = a.qstart[seq + 1] - qs;
+  const int q_len = qe - qs;
   if (m0 >= q_len) return;  // the whole workgroup: this sub-tile has no queries
-  const int ctx = min(a.ctx[seq], a.bt_width * 16);
+  const int ctx = min(ctx_in, a.bt_width * 16);
   const int base_pos = ctx - q_len;  // absolute position of query 0
   const int kv_end = max(0, min(ctx, base_pos + m0 + POS));
   // This unit's key blocks [kbeg, kend): all of them, or its piece's share.
@@ -238,17 +278,6 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // base + 16 l), so each lane loads the chunk that the swizzle puts in its
   // slot. fp16 V goes the same way; bf16 V passes through registers for
   // the fp16 conversion.
-  const int32_t* btrow = a.bt + seq * a.bt_sb;
-  const int last_page = (kv_end + 15) / 16 - 1;
-  auto load_pages = [&](int blk) {
-    int raw[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) raw[i] = scalar_load_i32(btrow, min(4 * blk + i, last_page));
-    BlockPages p;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p.id[i] = static_cast<uint32_t>(raw[i]) < static_cast<uint32_t>(a.num_blocks) ? raw[i] : 0;
-    return p;
-  };
   const char* kbytes = reinterpret_cast<const char*>(a.kc + static_cast<int64_t>(kvh) * a.c_sh);
   const char* vbytes = reinterpret_cast<const char*>(a.vc + static_cast<int64_t>(kvh) * a.c_sh);
   const uint32_t page_bytes = static_cast<uint32_t>(a.c_sb * 2);  // below 2^31 (host check)
@@ -436,12 +465,9 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // one barrier, which also waits for the K copies. The page ids of a block
   // are read one iteration before its loads are issued.
   Scores sa, sb;
-  BlockPages pg_v = load_pages(kbeg + 1);  // pages of V(kb + 1)
-  BlockPages pg_k = load_pages(kbeg + 2);  // pages of K(kb + 2)
-  if (kend > kbeg) {
-    const BlockPages pg0 = load_pages(kbeg);
-    issue_v(pg0, kbeg, IntC<0>{});
-    dma_k(pg0, kbeg, IntC<0>{});
+  if (kend > kbeg) {  // (then kbeg = kb0)
+    issue_v(pg_first, kbeg, IntC<0>{});
+    dma_k(pg_first, kbeg, IntC<0>{});
     // K(kbeg + 1) goes with the first block's loads (slot 1 is free), so the
     // first barrier waits for both at once. Past the context it reads zeros;
     // past the piece it is never read.
