@@ -261,10 +261,14 @@ int64_t nimbus_int8_matmul_workspace_bytes(int64_t m, int32_t n, int32_t k);
  *   y[i, j] = dtype(fp32(sum_k x[i, k] * w_q[j, k]) * scale[j])
  * x [m, k] and y [m, n] in dtype with row strides x_stride / y_stride
  * (elements); w_q int8 [n, k] with row stride w_stride (bytes); scale [n]
- * in dtype. n must be a multiple of 4 and k of 16; x, w_q and y 16-byte
- * aligned, scale 8-byte aligned, x_stride a multiple of 8, w_stride of 16,
- * y_stride of 4; x and w_q each under 2 GiB. The summation order over k
- * depends only on the shape, so equal inputs give equal outputs.
+ * in dtype; x, scale and y aligned to their 2-byte elements. Any shape runs,
+ * as the Triton kernel's masked tiles take any shape: the tiled kernel when
+ * n is a multiple of 4 and k of 16, x, w_q and y are 16-byte aligned, scale
+ * 8-byte aligned, x_stride a multiple of 8, w_stride of 16, y_stride of 4,
+ * x and w_q each under 2 GiB and m at most 2^21; otherwise a general kernel
+ * (one thread per output, k in order; for shapes no model layer has, not for
+ * speed, and it needs no workspace). Either way the summation order over k
+ * depends only on the shape and layout, so equal inputs give equal outputs.
  */
 int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w_q, int64_t w_stride, const void* scale,
                        void* y, int64_t y_stride, int64_t m, int32_t n, int32_t k, void* workspace,
@@ -277,10 +281,13 @@ int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w_q, int64_t
  * streams the weights in 1 KB contiguous pieces). Packed layout: block
  * (nb, kc) of [ceil(n/16)][ceil(k/64)] is 1024 bytes; bytes 16 l .. 16 l + 15
  * of a block hold row 16 nb + l % 16, columns 64 kc + 16 (l / 16) .. +16,
- * zero padded past n and k. n a multiple of 4, k of 8; x, w_packed and y
- * 16-byte aligned, scale 8-byte aligned; x_stride a multiple of 8,
- * y_stride of 4. The workspace rule is nimbus_int8_matmul's, sized by
- * nimbus_int8_matmul_packed_workspace_bytes.
+ * zero padded past n and k. The tiled kernel runs when n is a multiple of
+ * 4 and k of 8, x, w_packed and y are 16-byte aligned, scale 8-byte aligned,
+ * x_stride a multiple of 8 and y_stride of 4 (with nimbus_int8_matmul's size
+ * limits); any other call runs the general kernel on the packed layout. The
+ * workspace rule is nimbus_int8_matmul's, sized by
+ * nimbus_int8_matmul_packed_workspace_bytes (0 for shapes the tiled kernel
+ * does not take).
  */
 int64_t nimbus_int8_packed_weight_bytes(int32_t n, int32_t k);
 int nimbus_int8_pack_weight(const void* w_q, int64_t w_stride, int32_t n, int32_t k, void* out, void* stream);
@@ -296,7 +303,10 @@ int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const void* w_pac
  * workgroup (1, 2, 4 or 8, with ks * bm <= 128), splits of K (1..16) and
  * rows_per_wave 16-row blocks per wave (1 or 2). Any valid plan gives y to
  * fp32 summation order; the workspace is
- * nimbus_int8_matmul_packed_plan_workspace_bytes (-1 for an invalid plan).
+ * nimbus_int8_matmul_packed_plan_workspace_bytes (-1 for an invalid plan,
+ * and for a shape the tiled kernel does not take). A plan runs the tiled
+ * kernel only: a call it cannot take returns an error instead of falling
+ * back.
  */
 int64_t nimbus_int8_matmul_packed_plan_workspace_bytes(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
                                                        int32_t splits, int32_t rows_per_wave);

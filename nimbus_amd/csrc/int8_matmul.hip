@@ -628,12 +628,98 @@ static int launch_packed_dt(const GemmArgs& a, const PackPlan& p, hipStream_t s)
   }
 }
 
+// Any shape, stride and element alignment: the path of the calls the tiled
+// kernels above do not take (n not a multiple of 4, k not a multiple of 16
+// (row-major) or 8 (packed), operands past 2 GiB or off their 16-byte
+// alignment), as the Triton kernel's masked tiles take any shape. One thread
+// per (token, output channel), k summed in order with fp32 FMAs, so equal
+// inputs give equal outputs here too; it reads each weight once per token
+// and is meant for shapes no model layer has, not for speed.
+struct GeneralArgs {
+  const uint16_t* x;
+  int64_t sx;
+  const int8_t* w;
+  int64_t sw;  // row stride in bytes (row-major); unused for the packed layout
+  const uint16_t* scale;
+  uint16_t* y;
+  int64_t sy;
+  int64_t M;
+  int32_t N, K;
+};
+
+constexpr int kGeneralThreads = 256;
+constexpr int kGeneralRowsMax = 4096;  // grid.y; token rows beyond it are strided
+
+template <bool PACKED>
+__device__ __forceinline__ int8_t general_weight(const GeneralArgs& a, int n, int k) {
+  if constexpr (PACKED) {
+    const int64_t kc = (a.K + 63) / 64;
+    const int64_t block = static_cast<int64_t>(n / 16) * kc + k / 64;
+    return a.w[block * 1024 + 16 * (16 * ((k % 64) / 16) + n % 16) + k % 16];
+  } else {
+    return a.w[static_cast<int64_t>(n) * a.sw + k];
+  }
+}
+
+template <int DT, bool PACKED>
+__global__ __launch_bounds__(kGeneralThreads) void int8_matmul_general_kernel(GeneralArgs a) {
+  const int n = blockIdx.x * kGeneralThreads + threadIdx.x;
+  if (n >= a.N) return;
+  const float sc = Elem<DT>::to_f32(a.scale[n]);
+  for (int64_t m = blockIdx.y; m < a.M; m += gridDim.y) {
+    const uint16_t* xr = a.x + m * a.sx;
+    float acc = 0.f;
+    for (int k = 0; k < a.K; ++k)
+      acc = __builtin_fmaf(Elem<DT>::to_f32(xr[k]), static_cast<float>(general_weight<PACKED>(a, n, k)), acc);
+    a.y[m * a.sy + n] = Elem<DT>::from_f32(acc * sc);
+  }
+}
+
+template <bool PACKED>
+static int launch_general(const GeneralArgs& a, int32_t dtype, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>((a.N + kGeneralThreads - 1) / kGeneralThreads),
+                  static_cast<unsigned>(a.M < kGeneralRowsMax ? a.M : kGeneralRowsMax));
+  if (dtype == kFloat16) {
+    hipLaunchKernelGGL((int8_matmul_general_kernel<kFloat16, PACKED>), grid, dim3(kGeneralThreads), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((int8_matmul_general_kernel<kBFloat16, PACKED>), grid, dim3(kGeneralThreads), 0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+static GeneralArgs general_args(const void* x, int64_t x_stride, const void* w, int64_t w_stride, const void* scale,
+                                void* y, int64_t y_stride, int64_t m, int32_t n, int32_t k) {
+  GeneralArgs g;
+  g.x = static_cast<const uint16_t*>(x);
+  g.sx = x_stride;
+  g.w = static_cast<const int8_t*>(w);
+  g.sw = w_stride;
+  g.scale = static_cast<const uint16_t*>(scale);
+  g.y = static_cast<uint16_t*>(y);
+  g.sy = y_stride;
+  g.M = m;
+  g.N = n;
+  g.K = k;
+  return g;
+}
+
+// Element alignment, the one layout requirement the general kernel has.
+static bool elements_aligned(const void* x, const void* scale, const void* y) {
+  return ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(scale) | reinterpret_cast<uintptr_t>(y)) %
+          2) == 0;
+}
+
+// Shapes the tiled kernels take (the workspace queries follow them).
+static bool rowmajor_shape_ok(int32_t n, int32_t k) { return n % 4 == 0 && k % 16 == 0; }
+static bool packed_shape_ok(int32_t n, int32_t k) { return n % 4 == 0 && k % 8 == 0; }
+
 }  // namespace nimbus
 
 using namespace nimbus;
 
 extern "C" int64_t nimbus_int8_matmul_workspace_bytes(int64_t m, int32_t n, int32_t k) {
   if (m < 0 || n <= 0 || k <= 0) return -1;
+  if (!rowmajor_shape_ok(n, k)) return 0;  // the general kernel
   int32_t splits = 1, ksplit = 0;
   gemm_split(m, n, k, &splits, &ksplit);
   return splits > 1 ? static_cast<int64_t>(splits) * m * n * 4 : 0;
@@ -644,19 +730,22 @@ extern "C" int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w
                                   void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream) {
   if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
   if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
-  if (n % 4 != 0 || k % 16 != 0) return NIMBUS_ERR_UNSUPPORTED;
-  if (m > (int64_t{1} << 21)) return NIMBUS_ERR_UNSUPPORTED;  // token tiles fit grid.z
   if (m == 0) return NIMBUS_OK;
   if (!x || !w_q || !scale || !y) return NIMBUS_ERR_INVALID;
   if (x_stride < k || w_stride < k || y_stride < n) return NIMBUS_ERR_INVALID;
-  // Buffer offsets are 32-bit: each operand must span less than 2 GiB.
+  if (!elements_aligned(x, scale, y)) return NIMBUS_ERR_ALIGNMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // The tiled kernel: token tiles fit grid.z, buffer offsets are 32-bit (each
+  // operand under 2 GiB), 16-byte rows and operands.
   const int64_t x_bytes = ((m - 1) * x_stride + k) * 2;
   const int64_t w_bytes = (static_cast<int64_t>(n) - 1) * w_stride + k;
-  if (x_bytes >= (int64_t{1} << 31) || w_bytes >= (int64_t{1} << 31)) return NIMBUS_ERR_UNSUPPORTED;
-  if (x_stride % 8 != 0 || w_stride % 16 != 0 || y_stride % 4 != 0) return NIMBUS_ERR_ALIGNMENT;
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_q) | reinterpret_cast<uintptr_t>(y)) % 16 != 0 ||
-      reinterpret_cast<uintptr_t>(scale) % 8 != 0)
-    return NIMBUS_ERR_ALIGNMENT;
+  const bool tiled = rowmajor_shape_ok(n, k) && m <= (int64_t{1} << 21) && x_bytes < (int64_t{1} << 31) &&
+                     w_bytes < (int64_t{1} << 31) && x_stride % 8 == 0 && w_stride % 16 == 0 && y_stride % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_q) |
+                      reinterpret_cast<uintptr_t>(y)) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(scale) % 8 == 0;
+  if (!tiled)
+    return launch_general<false>(general_args(x, x_stride, w_q, w_stride, scale, y, y_stride, m, n, k), dtype, s);
   GemmArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.sx = static_cast<int32_t>(x_stride);
@@ -675,7 +764,6 @@ extern "C" int nimbus_int8_matmul(const void* x, int64_t x_stride, const void* w
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return NIMBUS_ERR_WORKSPACE;
   if (need > 0 && reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
   a.part = static_cast<float*>(workspace);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   return dtype == kFloat16 ? launch_gemm_dt<kFloat16>(a, s) : launch_gemm_dt<kBFloat16>(a, s);
 }
 
@@ -698,6 +786,7 @@ extern "C" int nimbus_int8_pack_weight(const void* w_q, int64_t w_stride, int32_
 
 extern "C" int64_t nimbus_int8_matmul_packed_workspace_bytes(int64_t m, int32_t n, int32_t k) {
   if (m < 0 || n <= 0 || k <= 0) return -1;
+  if (!packed_shape_ok(n, k)) return 0;  // the general kernel
   const PackPlan p = packed_plan(m, n, k);
   return p.splits > 1 ? static_cast<int64_t>(p.splits) * m * n * 4 : 0;
 }
@@ -707,19 +796,26 @@ static int packed_impl(const void* x, int64_t x_stride, const void* w_packed, co
                        int64_t workspace_bytes, int32_t dtype, void* stream) {
   if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
   if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
-  if (n % 4 != 0 || k % 8 != 0) return NIMBUS_ERR_UNSUPPORTED;
-  if (m > (int64_t{1} << 21)) return NIMBUS_ERR_UNSUPPORTED;  // token tiles fit grid.z
+  if (forced && !packed_shape_ok(n, k)) return NIMBUS_ERR_UNSUPPORTED;  // plans are the tiled kernel's
   if (m == 0) return NIMBUS_OK;
   if (!x || !w_packed || !scale || !y) return NIMBUS_ERR_INVALID;
   if (x_stride < k || y_stride < n) return NIMBUS_ERR_INVALID;
+  if (!elements_aligned(x, scale, y)) return NIMBUS_ERR_ALIGNMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t x_bytes = ((m - 1) * x_stride + k) * 2;
   const int64_t w_bytes = packed_bytes(n, k);
-  if (x_bytes >= (int64_t{1} << 31) || w_bytes >= (int64_t{1} << 31)) return NIMBUS_ERR_UNSUPPORTED;
-  if (x_stride % 8 != 0 || y_stride % 4 != 0) return NIMBUS_ERR_ALIGNMENT;
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed) | reinterpret_cast<uintptr_t>(y)) %
-              16 != 0 ||
-      reinterpret_cast<uintptr_t>(scale) % 8 != 0)
-    return NIMBUS_ERR_ALIGNMENT;
+  const bool tiled = packed_shape_ok(n, k) && m <= (int64_t{1} << 21) && x_bytes < (int64_t{1} << 31) &&
+                     w_bytes < (int64_t{1} << 31) && x_stride % 8 == 0 && y_stride % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed) |
+                      reinterpret_cast<uintptr_t>(y)) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(scale) % 8 == 0;
+  if (!tiled) {
+    if (forced) {
+      const bool too_big = m > (int64_t{1} << 21) || x_bytes >= (int64_t{1} << 31) || w_bytes >= (int64_t{1} << 31);
+      return too_big ? NIMBUS_ERR_UNSUPPORTED : NIMBUS_ERR_ALIGNMENT;
+    }
+    return launch_general<true>(general_args(x, x_stride, w_packed, 0, scale, y, y_stride, m, n, k), dtype, s);
+  }
   GemmArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.sx = static_cast<int32_t>(x_stride);
@@ -740,7 +836,6 @@ static int packed_impl(const void* x, int64_t x_stride, const void* w_packed, co
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) return NIMBUS_ERR_WORKSPACE;
   if (need > 0 && reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
   a.part = static_cast<float*>(workspace);
-  hipStream_t s = static_cast<hipStream_t>(stream);
   return dtype == kFloat16 ? launch_packed_dt<kFloat16>(a, plan, s) : launch_packed_dt<kBFloat16>(a, plan, s);
 }
 
@@ -779,7 +874,8 @@ extern "C" int64_t nimbus_int8_matmul_packed_plan_workspace_bytes(int64_t m, int
                                                                   int32_t ks, int32_t splits,
                                                                   int32_t rows_per_wave) {
   PackPlan p;
-  if (m < 0 || n <= 0 || k <= 0 || !make_plan(m, n, k, bm, ks, splits, rows_per_wave, &p)) return -1;
+  if (m < 0 || n <= 0 || k <= 0 || !packed_shape_ok(n, k) || !make_plan(m, n, k, bm, ks, splits, rows_per_wave, &p))
+    return -1;
   return p.splits > 1 ? static_cast<int64_t>(p.splits) * m * n * 4 : 0;
 }
 

@@ -45,8 +45,6 @@ def int8_matmul(x: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor, out: to
         raise ValueError(f"scale must be [{n}] in x's dtype")
     if not (x.is_cuda and w_q.is_cuda and scale.is_cuda):
         raise ValueError("int8_matmul runs on the GPU only")
-    if n % 4 != 0 or k % 16 != 0:
-        raise NotImplementedError(f"N {n} must be a multiple of 4 and K {k} of 16")
     shape = x.shape
     x2 = x.reshape(-1, k)
     if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
@@ -194,8 +192,6 @@ def int8_matmul_packed(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Ten
         raise ValueError(f"scale must be [{n}] in x's dtype")
     if not (x.is_cuda and w_packed.is_cuda and scale.is_cuda):
         raise ValueError("int8_matmul_packed runs on the GPU only")
-    if n % 4 != 0 or k % 8 != 0:
-        raise NotImplementedError(f"N {n} must be a multiple of 4 and K {k} of 8")
     shape = x.shape
     x2 = x.reshape(-1, k)
     if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
@@ -212,7 +208,8 @@ def int8_matmul_packed(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Ten
     lib = _lib.load()
     scale = scale.contiguous()
     key = (m_bucket(m), n, k, x.dtype, x.device.index)
-    if key not in _TUNED and AUTOTUNE and not torch.cuda.is_current_stream_capturing():
+    # (plans are the tiled kernel's: shapes it does not take run the general kernel untuned)
+    if key not in _TUNED and AUTOTUNE and n % 4 == 0 and k % 8 == 0 and not torch.cuda.is_current_stream_capturing():
         _TUNED[key] = _tune(x2, w_packed, scale, y, n, k, lib)
     plan = _TUNED.get(key)
     if plan is not None and lib.nimbus_int8_matmul_packed_plan_workspace_bytes(m, n, k, *plan) < 0:

@@ -190,21 +190,24 @@ def test_rms_norm_rejects_before_launch():
 
 
 def test_int8_matmul_rejects_before_launch():
-    """Shapes outside the kernel, null pointers and a missing split-K
-    workspace return an error code without touching memory."""
+    """Null pointers, misaligned elements, short strides and a missing
+    split-K workspace return an error code without touching memory; shapes
+    the tiled kernel does not take need no workspace (the general kernel)."""
     lib = _lib.load()
     f = lib.nimbus_int8_matmul
     ws = lib.nimbus_int8_matmul_workspace_bytes
     args = lambda m, n, k, **kw: dict(x=DUMMY, xs=k, w=DUMMY, wsd=k, s=DUMMY, y=DUMMY, ys=n, m=m, n=n, k=k,
                                       ws=None, wsb=0, dt=0, stream=None) | kw
     call = lambda **kw: f(*kw.values())
-    assert call(**args(4, 4098, 2048)) == _lib.NIMBUS_ERR_UNSUPPORTED  # n % 4
-    assert call(**args(4, 4096, 2040)) == _lib.NIMBUS_ERR_UNSUPPORTED  # k % 16
+    assert call(**args(4, 4098, 2048, x=None)) == _lib.NIMBUS_ERR_INVALID  # n % 4: checked like any shape
+    assert call(**args(4, 4096, 2040, y=None)) == _lib.NIMBUS_ERR_INVALID  # k % 16
+    assert ws(4, 4098, 2048) == 0 and ws(4, 4096, 2040) == 0  # the general kernel takes no workspace
     assert call(**args(4, 4096, 2048, dt=5)) == _lib.NIMBUS_ERR_UNSUPPORTED
     assert call(**args(0, 4096, 2048)) == 0
     assert call(**args(4, 4096, 2048, x=None)) == _lib.NIMBUS_ERR_INVALID
     assert call(**args(4, 4096, 2048, xs=2044)) == _lib.NIMBUS_ERR_INVALID  # stride below k
-    assert call(**args(4, 4096, 2048, x=DUMMY + 8)) == _lib.NIMBUS_ERR_ALIGNMENT
+    assert call(**args(4, 4096, 2048, x=DUMMY + 1)) == _lib.NIMBUS_ERR_ALIGNMENT  # not on a 2-byte element
+    assert call(**args(4, 4096, 2048, s=DUMMY + 3)) == _lib.NIMBUS_ERR_ALIGNMENT
     assert ws(4, 4096, 2048) > 0  # 32 channel tiles: K is split, so a workspace is needed
     assert call(**args(4, 4096, 2048)) == _lib.NIMBUS_ERR_WORKSPACE
     assert ws(300, 11264, 2048) == 0  # 88 x 5 tiles fill the chip: no split
@@ -228,6 +231,9 @@ def test_int8_explicit_plan_workspace_and_validation():
     assert ws(64, 28672, 4096, 64, 2, 1, 2) == 0
     for bad in [(48, 1, 1, 1), (64, 4, 1, 1), (16, 3, 1, 1), (16, 1, 17, 1), (16, 1, 1, 0), (16, 1, 1, 3)]:
         assert ws(64, 4096, 4096, *bad) == -1, bad
+    # shapes the tiled kernel does not take have no plan, and the default call needs no workspace
+    assert ws(64, 4098, 4096, 64, 2, 1, 1) == -1 and ws(64, 4096, 4092, 64, 2, 1, 1) == -1
+    assert lib.nimbus_int8_matmul_packed_workspace_bytes(64, 4098, 4096) == 0
 
 
 def test_prefill_pieces_checks():

@@ -5,7 +5,9 @@ rtol 1e-2 of fp32(x @ w_q^T) * scale rounded to the element type, on its
 matrix of M in {1, 7, 64, 300} and TinyLlama's projection shapes, in fp16.
 Added: bf16 and Llama-3-8B shapes, an exact check on small integers (pins
 the int8 -> fp16/bf16 widening bit for bit), shapes whose N and K leave
-partial tiles and steps, strided activations, and repeatability. Every
+partial tiles and steps, shapes and layouts only the general kernel takes
+(any N and K, as the Triton kernel's masked tiles), strided activations,
+and repeatability. Every
 product check runs on both weight layouts: row-major w_q (int8_matmul) and
 the tile order Int8Linear packs (int8_matmul_packed).
 """
@@ -15,6 +17,7 @@ from __future__ import annotations
 import pytest
 import torch
 
+from nimbus_amd import _lib
 from nimbus_amd.kernels.int8_matmul import (int8_matmul, int8_matmul_packed, int8_matmul_workspace_bytes,
                                             pack_int8_weight, unpack_int8_weight)
 from nimbus_amd.quant import Int8Linear, quantize_weight
@@ -70,8 +73,6 @@ def test_small_integers_are_exact(dtype, m, n, k, packed):
     sum is exact in fp32, so the kernel must equal the float64 product
     rounded once, whatever the tiling or K split."""
     announce(f"int8_matmul exact {dtype} m={m} n={n} k={k} packed={packed}")
-    if not packed and k % 16:
-        pytest.skip("the row-major kernel takes K in multiples of 16")
     g = torch.Generator(device="cuda").manual_seed(m * n + k)
     x = torch.randint(-3, 4, (m, k), generator=g, device="cuda").to(dtype)
     q = torch.randint(-127, 128, (n, k), generator=g, device="cuda").to(torch.int8)
@@ -100,6 +101,58 @@ def test_strided_rows_leading_dims_and_repeatability():
     torch.testing.assert_close(a.cpu(), want, atol=2e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("m,n,k", [(7, 4098, 2040), (3, 37, 4099), (1, 6, 13), (5, 130, 2056)])
+def test_any_shape_runs_like_the_masked_triton_tiles(dtype, m, n, k, packed):
+    """The reference's Triton kernel masks its tiles, so it takes any N and
+    K; shapes the tiled kernels do not take (N not a multiple of 4, K not of
+    16 row-major / 8 packed) run the general kernel, to the same bar, with
+    the same bits on a repeat."""
+    announce(f"int8_matmul any shape {dtype} m={m} n={n} k={k} packed={packed}")
+    x, q, s = _case(m, n, k, dtype, m + 3 * n + k)
+    got = _mm(x, q, s, packed)
+    again = _mm(x, q, s, packed)
+    want = reference.int8_matmul(x.cpu(), q.cpu(), s.cpu())
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
+    torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_unaligned_activations_take_the_general_kernel(packed):
+    """Through the C ABI (the Python wrappers copy such an x first): x one
+    element into its buffer (2-byte aligned, not 16) with an odd row stride
+    and y likewise, so the tiled kernels' alignment does not hold and the
+    general kernel runs; against the oracle and the aligned call."""
+    announce(f"int8_matmul unaligned x, y through the C ABI packed={packed}")
+    g = torch.Generator(device="cuda").manual_seed(9)
+    m, n, k = 9, 512, 1024
+    wide = torch.randn(m, k + 3, generator=g, device="cuda").half()
+    x = wide[:, 1:1 + k]
+    ybuf = torch.zeros(m, n + 3, dtype=torch.float16, device="cuda")
+    y = ybuf[:, 1:1 + n]
+    assert x.data_ptr() % 16 != 0 and x.stride(0) % 8 != 0 and y.data_ptr() % 16 != 0
+    w = (torch.randn(n, k, generator=g, device="cuda") * 0.02).half()
+    q, s = quantize_weight(w)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    if packed:
+        wp = pack_int8_weight(q)
+        rc = lib.nimbus_int8_matmul_packed(x.data_ptr(), x.stride(0), wp.data_ptr(), s.data_ptr(), y.data_ptr(),
+                                           y.stride(0), m, n, k, None, 0, _lib.dtype_code(x.dtype), stream)
+    else:
+        rc = lib.nimbus_int8_matmul(x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0), s.data_ptr(), y.data_ptr(),
+                                    y.stride(0), m, n, k, None, 0, _lib.dtype_code(x.dtype), stream)
+    assert rc == 0
+    want = reference.int8_matmul(x.cpu(), q.cpu(), s.cpu())
+    aligned = _mm(x.contiguous(), q, s, packed)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(y.cpu(), want, atol=2e-2, rtol=1e-2)
+    torch.testing.assert_close(y, aligned, atol=2e-3, rtol=2e-3)
+    assert torch.all(ybuf[:, 0] == 0) and torch.all(ybuf[:, n + 1:] == 0)  # nothing outside y written
+
+
 def test_int8_linear_matches_dequantized_linear():
     """Int8Linear (nimbus/quant/int8.py:32-47) against F.linear with the
     dequantized weight, the reference module's own definition."""
@@ -113,6 +166,14 @@ def test_int8_linear_matches_dequantized_linear():
     torch.cuda.synchronize()
     torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
     assert mod.weight_q.dtype == torch.int8 and mod.weight_q.shape == (512, 2048)
+    # features that leave partial tiles and an odd K (the general kernel)
+    lin = torch.nn.Linear(1027, 301, bias=False).cuda().half()
+    mod = Int8Linear(lin)
+    x = torch.randn(3, 1027, device="cuda").half()
+    got = mod(x)
+    want = reference.int8_matmul(x.cpu(), mod.weight_q.cpu(), mod.scale.cpu())
+    torch.cuda.synchronize()
+    torch.testing.assert_close(got.cpu(), want, atol=2e-2, rtol=1e-2)
 
 
 def test_zero_rows_and_explicit_workspace():
