@@ -69,6 +69,7 @@ constexpr int kPage = 16;             // tokens per page (the only block size)
 // configs 3 and 5 unchanged.
 constexpr int kMinPagesPerWave = 2;
 constexpr int kMaxDecodeBatch = 4096; // LDS holds the batch's page prefix sum
+constexpr int kRegPrefixBatch = 64;   // up to this batch the prefix lives in registers, a lane per sequence
 constexpr int kWavesPerCU = 8;        // two waves of the page kernel per SIMD
 constexpr int kMaxWgWaves = 8;        // waves (kv-head groups) per workgroup
 constexpr int kSyncPages = 4;         // pages between the workgroup's barriers
@@ -220,9 +221,20 @@ __device__ __forceinline__ int v_pos(int r, int c) {
 // streaming measured 5-6% faster there (config 3's page pass 86.6-88.0 us
 // against 92.1-93.3); with two chunks the second chunk's reads of a page hit
 // the L2 the first chunk filled, so those launches load ordinarily.
-template <int DT, int D, bool STREAM>
+// STREAM: K/V pages loaded nontemporally (a launch with one column chunk
+// reads every page once). REGP: the batch has at most kRegPrefixBatch
+// sequences and its page prefix lives in registers (a compile-time choice:
+// with both paths in one kernel the waits the LDS path needs are placed on
+// the register path too).
+template <int DT, int D, bool STREAM, bool REGP>
 __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(
     DecodeArgs a) {
+  // (takes the kernel arguments the first page loads need, so that their
+  // loads go out with the first ones instead of after the prefix, a round
+  // trip of their own)
+  asm volatile("" ::"s"(a.q), "s"(a.q_sb), "s"(a.q_sh), "s"(a.kc), "s"(a.vc), "s"(a.c_sb), "s"(a.c_st), "s"(a.c_sh),
+               "s"(a.bt), "s"(a.bt_sb), "s"(a.num_blocks), "s"(a.ctx), "s"(a.B), "s"(a.nq), "s"(a.nwk), "s"(a.wgw),
+               "s"(a.wgc), "s"(a.max_ctx));
   constexpr int KK = D / 32;
   constexpr int NN = D / 16;              // 16-row blocks of O^T
   constexpr int LPT = D / 8;              // lanes per token row (16 bytes each)
@@ -251,11 +263,40 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
   const int back = a.nq - 1 - qj;  // keys this query sees fewer than the newest
   const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;  // partial-piece row
 
-  page_prefix(a, pre);
-  const int total = __builtin_amdgcn_readfirstlane(pre[a.B]);
-  if (blockIdx.x == 0 && wave == 0) {
-    for (int i = lane; i <= a.B; i += 64) a.pre_out[i] = pre[i];
+  // The batch's page prefix. Up to 64 sequences (REGP) every wave holds it in
+  // registers, lane i the pages of sequences 0..i (lanes past the batch:
+  // INT32_MAX): a page's sequence is then a ballot, and neither LDS nor a
+  // barrier stands between the context lengths and the page-id loads, which
+  // all go out together. A larger batch keeps it in LDS (page_prefix), the
+  // walk moving a cursor over it.
+  constexpr bool reg_prefix = REGP;
+  int incl = INT32_MAX;
+  int total;
+  if constexpr (reg_prefix) {
+    int v = lane < a.B ? pages_of(a, lane) : 0;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int t = __shfl_up(v, off, 64);
+      if (lane >= off) v += t;
+    }
+    if (lane < a.B) incl = v;
+    total = __builtin_amdgcn_readlane(v, a.B - 1);  // (the host launches no empty batch)
+    if (blockIdx.x == 0 && wave == 0) {
+      if (lane == 0) a.pre_out[0] = 0;
+      if (lane < a.B) a.pre_out[lane + 1] = v;
+    }
+  } else {
+    page_prefix(a, pre);
+    total = __builtin_amdgcn_readfirstlane(pre[a.B]);
+    if (blockIdx.x == 0 && wave == 0) {
+      for (int i = lane; i <= a.B; i += 64) a.pre_out[i] = pre[i];
+    }
   }
+  // Pages before sequence b (wave-uniform b <= B).
+  auto prefix_at = [&](int b) {
+    if constexpr (reg_prefix) return b == 0 ? 0 : __builtin_amdgcn_readlane(incl, b - 1);
+    else return pre[b];
+  };
   const int nw = active_waves(total, a.nwk);
   if (idx >= nw || total == 0) return;
   const int lo = slice_start(idx, nw, total);
@@ -279,7 +320,7 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
   // First sequence of the slice: the largest b with pre[b] <= lo; `cursor`
   // then only moves forward.
   int cursor = 0;
-  {
+  if constexpr (!reg_prefix) {
     int l = 0, h = a.B;
     while (h - l > 1) {
       const int mid = (l + h) >> 1;
@@ -288,12 +329,22 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
     }
     cursor = l;
   }
-  auto locate = [&](int y) {
-    PageRef r;
-    if (y < hi) {
+  // Sequence and page of flat page y < hi.
+  auto place = [&](int y, PageRef& r) {
+    if constexpr (reg_prefix) {
+      // sequences that end at or before page y (y < total: at most B - 1)
+      r.b = __builtin_popcountll(__builtin_amdgcn_ballot_w64(incl <= y));
+      r.p = __builtin_amdgcn_readfirstlane(y - prefix_at(r.b));
+    } else {
       while (pre[cursor + 1] <= y) ++cursor;
       r.b = __builtin_amdgcn_readfirstlane(cursor);
       r.p = __builtin_amdgcn_readfirstlane(y - pre[cursor]);
+    }
+  };
+  auto locate = [&](int y) {
+    PageRef r;
+    if (y < hi) {
+      place(y, r);
       r.ctx_raw = scalar_load(a.ctx, r.b);
       r.pid_raw = scalar_load(a.bt + r.b * a.bt_sb, r.p);
     } else {
@@ -324,7 +375,37 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
   // ref[i] describes page x + i of the step about to run.
   PageRef ref[kRing + 2];
 #pragma unroll
-  for (int i = 0; i < kRing + 2; ++i) ref[i] = locate(lo + i);
+  for (int i = 0; i < kRing + 2; ++i) ref[i] = PageRef{-1, 0, 0, 0};
+  {
+    // The first kRing + 2 pages' table entries and context lengths: lane i
+    // loads page lo + i's, two vector loads for all of them. As scalar loads
+    // (what the walk uses, so that they never wait behind its K/V loads)
+    // they took 3-12 us here on config 3's cold block tables, every wave of
+    // the chip missing the scalar caches at once; no K/V load is in flight
+    // yet for these to queue behind.
+    int vb = 0, vp = 0;
+    bool von = false;
+#pragma unroll
+    for (int i = 0; i < kRing + 2; ++i) {
+      if (lo + i < hi) {
+        place(lo + i, ref[i]);
+        if (lane == i) {
+          vb = ref[i].b;
+          vp = ref[i].p;
+          von = true;
+        }
+      }
+    }
+    const int vpid = von ? a.bt[static_cast<int64_t>(vb) * a.bt_sb + vp] : 0;
+    const int vctx = von ? a.ctx[vb] : 0;
+#pragma unroll
+    for (int i = 0; i < kRing + 2; ++i) {
+      if (lo + i < hi) {
+        ref[i].pid_raw = __builtin_amdgcn_readlane(vpid, i);
+        ref[i].ctx_raw = __builtin_amdgcn_readlane(vctx, i);
+      }
+    }
+  }
   PageBuf<D> buf[kRing];
 #pragma unroll
   for (int i = 0; i < kRing; ++i) {
@@ -442,7 +523,7 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
       // Finish the piece [seg0, x] of sequence cur.b.
       const int rb = cur.b;
       const float l = sum_across_groups(l_run);
-      const bool whole = seg0 == pre[rb] && x + 1 == pre[rb + 1];
+      const bool whole = seg0 == prefix_at(rb) && x + 1 == prefix_at(rb + 1);
       if (g_ok) {
         if (whole) {
           const float inv = l > 0.f ? 1.f / l : 0.f;  // a query that sees no key gives 0
@@ -629,10 +710,14 @@ template <int DT, int D>
 static int launch_decode(const DecodeArgs& a, int phases, hipStream_t stream) {
   if (phases & 1) {
     const size_t dyn = static_cast<size_t>(a.B + 1) * sizeof(int);
+    const dim3 grid(a.nwk * a.wgc), block(64 * a.wgw);
+    const bool regp = a.B <= kRegPrefixBatch;
     if (a.gchunks == 1) {
-      hipLaunchKernelGGL((paged_decode_kernel<DT, D, true>), dim3(a.nwk * a.wgc), dim3(64 * a.wgw), dyn, stream, a);
+      if (regp) hipLaunchKernelGGL((paged_decode_kernel<DT, D, true, true>), grid, block, dyn, stream, a);
+      else hipLaunchKernelGGL((paged_decode_kernel<DT, D, true, false>), grid, block, dyn, stream, a);
     } else {
-      hipLaunchKernelGGL((paged_decode_kernel<DT, D, false>), dim3(a.nwk * a.wgc), dim3(64 * a.wgw), dyn, stream, a);
+      if (regp) hipLaunchKernelGGL((paged_decode_kernel<DT, D, false, true>), grid, block, dyn, stream, a);
+      else hipLaunchKernelGGL((paged_decode_kernel<DT, D, false, false>), grid, block, dyn, stream, a);
     }
   }
   if (phases & 2) {
