@@ -239,8 +239,12 @@ int nimbus_paged_verify(int32_t queries_per_seq, const void* q, int64_t q_stride
  *   s = x + residual (in the element type; written to residual_out),
  *   out = weight * dtype(s * rsqrt(mean(s^2) + eps)) (mean and scale in fp32).
  * residual == NULL is plain RMSNorm of x (residual_out unused). Rows are
- * [rows, cols] with unit element stride and the given row strides; cols must
- * be a multiple of 8 and at most 8192.
+ * [rows, cols] with unit element stride and the given row strides, pointers
+ * aligned to their 2-byte elements. Any cols runs, as the Triton kernel's
+ * masked block takes any row: the chunked kernel when cols is a multiple of
+ * 8 and at most 8192, every pointer 16-byte aligned and every row stride a
+ * multiple of 8; otherwise a general kernel (an element per thread, for rows
+ * no Llama layer has).
  */
 int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
                         const void* weight, void* out, int64_t out_stride, void* residual_out,

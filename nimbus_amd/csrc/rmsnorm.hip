@@ -190,6 +190,60 @@ static int launch_norm(const NormArgs& a, hipStream_t s) {
   }
 }
 
+// Any row length, stride and element alignment: the path of the calls the
+// chunked kernel above does not take (a row length not a multiple of 8 or
+// past 8192, rows off their 16-byte alignment), as the Triton kernel's
+// masked block takes any row. One 256-thread workgroup per row at a time,
+// an element per thread per pass: the sum of squares of the rounded sums,
+// reduced as above, then a second pass that forms the sum again (it does not
+// read back what the first pass stored) and writes the output.
+template <int DT>
+__device__ __forceinline__ float elem_f32(uint16_t v) {
+  return Elem<DT>::to_f32(v);
+}
+
+template <int DT, bool RES>
+__global__ __launch_bounds__(256) void add_rms_norm_general_kernel(NormArgs a) {
+  const int wave = static_cast<int>(threadIdx.x) / 64;
+  const int lane = threadIdx.x % 64;
+  __shared__ float part[2][4];
+  int par = 0;
+  auto sum_at = [&](int64_t row, int c) {  // dtype(x + r), as a float
+    const float xv = elem_f32<DT>(a.x[row * a.sx + c]);
+    if constexpr (RES) return elem_f32<DT>(Elem<DT>::from_f32(xv + elem_f32<DT>(a.r[row * a.sr + c])));
+    else return xv;
+  };
+  for (int row = blockIdx.x; row < a.rows; row += gridDim.x) {
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < a.cols; c += 256) {
+      const float v = sum_at(row, c);
+      if constexpr (RES) a.rout[static_cast<int64_t>(row) * a.sro + c] = Elem<DT>::from_f32(v);
+      ss = __builtin_fmaf(v, v, ss);
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) part[par][wave] = ss;
+    __syncthreads();
+    ss = (part[par][0] + part[par][1]) + (part[par][2] + part[par][3]);
+    par ^= 1;
+    const float inv = 1.f / __builtin_sqrtf(ss / static_cast<float>(a.cols) + a.eps);
+    for (int c = threadIdx.x; c < a.cols; c += 256) {
+      const float y = elem_f32<DT>(Elem<DT>::from_f32(sum_at(row, c) * inv));  // dtype(s * rsqrt(...))
+      a.out[static_cast<int64_t>(row) * a.so + c] = Elem<DT>::from_f32(elem_f32<DT>(a.w[c]) * y);
+    }
+  }
+}
+
+template <int DT>
+static int launch_norm_general(const NormArgs& a, hipStream_t s) {
+  const unsigned grid = static_cast<unsigned>(a.rows < kNormGrid ? a.rows : kNormGrid);
+  if (a.r) {
+    hipLaunchKernelGGL((add_rms_norm_general_kernel<DT, true>), dim3(grid), dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL((add_rms_norm_general_kernel<DT, false>), dim3(grid), dim3(256), 0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
 }  // namespace nimbus
 
 using namespace nimbus;
@@ -200,15 +254,16 @@ extern "C" int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* 
                                    void* stream) {
   if (rows < 0 || cols <= 0) return NIMBUS_ERR_INVALID;
   if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
-  if (cols % 8 != 0 || cols > 256 * kNormMaxChunksPerLane * 8) return NIMBUS_ERR_UNSUPPORTED;
   if (rows > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
   if (rows == 0) return NIMBUS_OK;
   if (!x || !weight || !out || (residual && !residual_out)) return NIMBUS_ERR_INVALID;
-  if ((x_stride | out_stride | (residual ? residual_stride | residual_out_stride : 0)) % 8 != 0)
-    return NIMBUS_ERR_ALIGNMENT;
-  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(out) |
-       reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(residual_out)) % 16 != 0)
-    return NIMBUS_ERR_ALIGNMENT;
+  const uintptr_t ptrs = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(weight) |
+                         reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual) |
+                         reinterpret_cast<uintptr_t>(residual_out);
+  if (ptrs % 2 != 0) return NIMBUS_ERR_ALIGNMENT;  // 2-byte elements
+  // The chunked kernel: rows of 16-byte chunks, at most 8192 elements.
+  const bool chunked = cols % 8 == 0 && cols <= 256 * kNormMaxChunksPerLane * 8 && ptrs % 16 == 0 &&
+                       (x_stride | out_stride | (residual ? residual_stride | residual_out_stride : 0)) % 8 == 0;
   NormArgs a;
   a.x = static_cast<const uint16_t*>(x);
   a.sx = x_stride;
@@ -223,5 +278,6 @@ extern "C" int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* 
   a.cols = cols;
   a.eps = eps;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!chunked) return dtype == kFloat16 ? launch_norm_general<kFloat16>(a, s) : launch_norm_general<kBFloat16>(a, s);
   return dtype == kFloat16 ? launch_norm<kFloat16>(a, s) : launch_norm<kBFloat16>(a, s);
 }

@@ -14,6 +14,8 @@ import torch
 
 from nimbus_amd import _lib
 
+# Rows the chunked kernel takes (a multiple of 8 elements, at most MAX_COLS);
+# any other length runs the library's general kernel.
 MAX_COLS = 8192
 
 
@@ -23,8 +25,6 @@ def _launch(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor
         raise ValueError(f"weight {tuple(weight.shape)} does not match rows of {n}")
     if x.dtype not in (torch.float16, torch.bfloat16) or weight.dtype != x.dtype:
         raise NotImplementedError("fp16 or bf16 x and weight of one dtype")
-    if n % 8 != 0 or n > MAX_COLS:
-        raise NotImplementedError(f"row length {n}: must be a multiple of 8 and at most {MAX_COLS}")
     if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype):
         raise ValueError("residual must match x's shape and dtype")
     if not (x.is_cuda and weight.is_cuda and (residual is None or residual.is_cuda)):

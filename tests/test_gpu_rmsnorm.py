@@ -4,7 +4,8 @@ The bar is the reference's own (tests/test_kernels.py:78-89 of Nimbus): the
 new residual is bit-exact, the normalised output within atol 4e-3, rtol 2e-3
 of nimbus/kernels/reference.py's rms_norm on the same inputs. Nimbus applies
 it to fp16 only; bf16 is held to it for all but 1e-5 of the elements and to
-rtol 2^-6 (see assert_norm_close).
+rtol 2^-6 (see assert_norm_close). Row lengths and layouts the chunked
+kernel does not take run the general kernel, to the same bar.
 """
 
 from __future__ import annotations
@@ -115,3 +116,42 @@ def test_inputs_are_not_modified_and_zero_rows():
     assert torch.equal(x, x0) and torch.equal(r, r0)
     y, res = add_rms_norm(x[:0], r[:0], w, 1e-5)
     assert y.shape == (0, 512) and res.shape == (0, 512)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("rows,cols", [(3, 777), (5, 12), (2, 16384), (4, 10001), (1, 1)])
+def test_any_row_length_runs_like_the_masked_triton_block(dtype, rows, cols):
+    """The reference's Triton kernel masks a power-of-two block, so it takes
+    any row length; lengths the chunked kernel does not take (not a multiple
+    of 8, or past 8192) run the general kernel, to the same bar, with the new
+    residual still bit-exact."""
+    announce(f"add_rms_norm any row length dtype={dtype} rows={rows} cols={cols}")
+    x, r, w = _inputs(rows, cols, dtype, rows * 11 + cols)
+    got_y, got_r = add_rms_norm(x, r, w, 1e-5)
+    want_y, want_r = reference.add_rms_norm(x.cpu(), r.cpu(), w.cpu(), 1e-5)
+    got = rms_norm(x, w, 1e-5)
+    want = reference.rms_norm(x.cpu(), w.cpu(), 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got_r.cpu()), _bits(want_r))
+    assert_norm_close(got_y.cpu(), want_y)
+    assert_norm_close(got.cpu(), want)
+
+
+def test_unaligned_rows_take_the_general_kernel():
+    """Through the wrapper with rows one element into their buffers (2-byte
+    aligned, not 16, odd row stride): the general kernel, against the oracle
+    and against the same rows made contiguous (the chunked kernel)."""
+    announce("add_rms_norm unaligned rows")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    wide_x = torch.randn(6, 2049, generator=g, device="cuda").half()
+    wide_r = torch.randn(6, 2051, generator=g, device="cuda").half()
+    x, r = wide_x[:, 1:2049], wide_r[:, 3:2051]
+    assert x.data_ptr() % 16 != 0 and x.stride(0) % 8 != 0
+    w = torch.randn(2048, generator=g, device="cuda").half()
+    got_y, got_r = add_rms_norm(x, r, w, 1e-5)
+    want_y, want_r = reference.add_rms_norm(x.cpu(), r.cpu(), w.cpu(), 1e-5)
+    al_y, al_r = add_rms_norm(x.contiguous(), r.contiguous(), w, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got_r.cpu()), _bits(want_r)) and torch.equal(got_r, al_r)
+    assert_norm_close(got_y.cpu(), want_y)
+    torch.testing.assert_close(got_y, al_y, atol=4e-3, rtol=2e-3)

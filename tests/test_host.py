@@ -123,9 +123,9 @@ def test_kernels_refuse_cpu_tensors():
 
 
 def test_rms_norm_wrapper_checks_shapes():
-    x = torch.zeros(3, 60, dtype=torch.float16)
-    with pytest.raises(NotImplementedError):
-        rmsnorm.rms_norm(x, torch.ones(60, dtype=torch.float16), 1e-5)
+    # any row length is taken (60 is not a multiple of 8: the general kernel); CPU tensors are refused
+    with pytest.raises(ValueError, match="GPU only"):
+        rmsnorm.rms_norm(torch.zeros(3, 60, dtype=torch.float16), torch.ones(60, dtype=torch.float16), 1e-5)
     with pytest.raises(NotImplementedError):
         rmsnorm.rms_norm(torch.zeros(2, 64), torch.ones(64), 1e-5)  # float32
     with pytest.raises(ValueError):
