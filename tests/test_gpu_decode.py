@@ -83,6 +83,22 @@ def test_lockstep_workgroup_shapes(heads, kv, d, batch, max_ctx):
     assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale), what="vs oracle")
 
 
+@pytest.mark.parametrize("batch", [1, 2, 63, 64, 65, 130])
+def test_prefix_in_registers_and_in_lds(batch):
+    """Up to 64 sequences the page prefix lives in registers (a lane per
+    sequence, a ballot per page); past that, in LDS. Both sides of the
+    boundary, with runs of one-page sequences (several sequences in one
+    wave's slice) between long ones, against the oracle."""
+    announce(f"decode prefix path B={batch}")
+    g = torch.Generator().manual_seed(batch)
+    ctx_lens = [int(c) for c in torch.randint(1, 1200, (batch,), generator=g)]
+    for i in range(0, batch, 3):
+        ctx_lens[i] = 1 + i % 17  # one page (up to 17 tokens: two)
+    q, k, v, ctx, bt, scale = _case(32, 8, 128, ctx_lens, torch.bfloat16, seed=batch + 1)
+    got = paged_decode_attention(q, k, v, ctx, bt, max(ctx_lens), scale)
+    assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale), what="vs oracle")
+
+
 def test_grid_width_does_not_change_results():
     """A wider grid (larger max_context, as under graph capture) only adds
     partitions that exit at once: results are bit-identical."""
