@@ -201,6 +201,7 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   int kb1 = scalar_load_i32(p_blk, 1);
   int slot = scalar_load_i32(p_blk, 2);
   asm volatile("" : "+s"(seq), "+s"(m_entry), "+s"(kb0), "+s"(kb1), "+s"(slot));
+  kb0 = max(kb0, 0);  // (a piece's first block; the page ids below are indexed from it)
   const int32_t* btrow = a.bt + seq * a.bt_sb;
   const int page_cap = a.bt_width - 1;
   auto load_raw = [&](int blk) {
