@@ -15,7 +15,8 @@
 //   (|w_q| <= 127 fits either type's significand);
 // - x's 64-k step for the workgroup's tokens is staged in LDS once and read
 //   by all 8 waves; its global loads ride the same kRing-deep register ring
-//   as the weights, so waiting for one never drains the other;
+//   as the weights, so waiting for one never drains the other (the
+//   tile-order kernel further down loads x straight into LDS instead);
 // - the k order inside a step is the same permutation for both operands, so
 //   one 16-byte weight load feeds two MFMAs: chunk 0 takes k = 16g + 0..7 of
 //   lane group g, chunk 1 takes k = 16g + 8..15 (the sum over k does not
@@ -24,6 +25,8 @@
 // workgroups: each writes its fp32 partial sums, and
 // int8_matmul_reduce_kernel adds them in split order (the result does not
 // depend on timing), scales and rounds.
+#include <type_traits>
+
 #include "common.h"
 #include "nimbus_attn_internal.h"
 
@@ -68,6 +71,12 @@ typedef _Float16 h16x2 __attribute__((ext_vector_type(2)));
 // LDS's active cycles; with this order, none.
 __device__ __forceinline__ int x_chunk(int t, int c) {
   return ((c >> 1) | ((c & 1) << 2)) ^ (t & 7);
+}
+
+// x_chunk's inverse: the chunk stored at position p of token t's row.
+__device__ __forceinline__ int x_chunk_at(int t, int p) {
+  const int u = p ^ (t & 7);
+  return ((u << 1) & 6) | (u >> 2);
 }
 
 // Eight int8 (two dwords) -> the eight fp16 / bf16 of an MFMA operand.
@@ -118,6 +127,39 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Waits until at most N of this wave's vector-memory loads are outstanding
+// (gfx9 s_waitcnt: vmcnt in bits 3:0 and 15:14; expcnt and lgkmcnt left at
+// their maxima, i.e. not waited for). Loads return in issue order, so every
+// load issued before the last N has landed.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds six bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// 16 bytes per lane from a buffer straight into LDS: lane l's land at
+// lds + 16 l (lds is the same for the whole wave). A non-template function,
+// so that the host pass, which cannot form the LDS pointer, only defers its
+// complaint about this body instead of dropping the kernels' host stubs.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, off, 0, 0, 0);
+}
+
+// Workgroup barrier for x loaded straight into LDS: each wave first waits
+// until its loads older than the last N have written LDS, so after the
+// barrier every wave's part of those steps is there. The compiler does not
+// count these loads against later LDS reads of the same array, and the
+// workgroup fence would wait for every load in flight (the weight ring
+// too), hence the count by hand; the signal fences keep the compiler from
+// moving LDS accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void dma_barrier() {
+  wait_vm<N>();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // Grid: (N / 128 channel tiles, splits, M / BM token tiles).
@@ -311,12 +353,17 @@ static int launch_gemm_dt(const GemmArgs& a, hipStream_t s) {
 // slices (RB x KS = 8, BM x KS <= 128); a wave computes RW row blocks (1 or
 // 2) from each x operand it reads. Waves of one group take interleaved 64-k
 // chunks and their sums are added in LDS at the end (fixed order), so narrow
-// matrices need no cross-workgroup split for small M. A step reads all of its
-// x operands from LDS at once and runs its MFMAs on weights converted during
-// the previous step, converting the next step's weights while they execute;
-// the workgroup meets at a barrier every second step.
+// matrices need no cross-workgroup split for small M. x goes from memory
+// straight into LDS (buffer loads with the LDS bit: no registers, no LDS
+// write instructions), kXLead steps ahead into a ring of kXBufs buffers. A
+// step reads all of its x operands from LDS at once and runs its MFMAs on
+// weights converted during the previous step, converting the next step's
+// weights while they execute; the workgroup meets at a barrier every second
+// step.
 
-constexpr int kPackRing = 6;  // steps of loads in flight
+constexpr int kPackRing = 6;  // steps of weight loads in flight
+constexpr int kXBufs = 8;     // x steps in LDS
+constexpr int kXLead = kXBufs - 2;  // x loaded this many steps ahead
 
 template <int BM, int KS, int RW>
 struct PackShape {
@@ -332,10 +379,15 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
   constexpr int RB = PackShape<BM, KS, RW>::RB;
   constexpr int XP = PackShape<BM, KS, RW>::XP;
   constexpr int XC = PackShape<BM, KS, RW>::XC;
-  static_assert((KS - 1) * RB * RW * CB * 1024 <= 4 * KS * BM * kXRow, "the k-slice sums fit the x buffers");
-  // Four x buffers: step s reads buffer s % 4 and stages x(s + 2), so one
-  // barrier every second step keeps writers off buffers still being read.
-  __shared__ __attribute__((aligned(16))) uint8_t xs[4][KS * BM * kXRow];
+  constexpr int XBUF = KS * BM * kXRow;             // bytes of one step of x
+  constexpr bool XSPARE = XP % kGemmThreads != 0;   // waves past XP load into a spare 1 KB
+  static_assert((KS - 1) * RB * RW * CB * 1024 <= kXBufs * XBUF, "the k-slice sums fit the x buffers");
+  static_assert(kXBufs * XBUF + (XSPARE ? 1024 : 0) <= 160 * 1024, "x ring fits LDS");
+  // Step s reads buffer s % kXBufs, and x(s + kXLead) is loaded into buffer
+  // (s - 2) % kXBufs, which step s - 2 read before the last barrier; one
+  // array, indexed at run time, so the compiler inserts no waits of its own
+  // for these loads (dma_barrier does).
+  __shared__ __attribute__((aligned(16))) uint8_t xs[kXBufs * XBUF + (XSPARE ? 1024 : 0)];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
@@ -365,44 +417,47 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                          wrsrc, on ? woff[j] + KS * 1024 * s : kOutOfRange, 0, 0));
   };
+  // Piece q = tid + 256 i of a step is token row q / 8 (k slice j, token
+  // tok) at LDS position q % 8 of that row, so a wave's 64 pieces fill 1 KB
+  // of LDS in lane order, as the LDS-bit load writes them; the swizzle is
+  // applied to the source instead (position q % 8 holds chunk x_chunk_at).
   uint32_t xoff[XC];
-  int xk[XC], xs_off[XC];
-  bool x_on[XC], x_mine[XC];
+  int xk[XC];
+  bool x_on[XC];
 #pragma unroll
   for (int i = 0; i < XC; ++i) {
     const int q = tid + kGemmThreads * i;
     const int j = q / (8 * BM);
     const int tok = (q % (8 * BM)) / 8;
-    const int ch = q % 8;
-    x_mine[i] = q < XP;
-    x_on[i] = x_mine[i] && m0 + tok < a.M;
-    xk[i] = 64 * (c0 + j) + 8 * ch;
+    x_on[i] = q < XP && m0 + tok < a.M;
+    xk[i] = 64 * (c0 + j) + 8 * x_chunk_at(tok, q % 8);
     xoff[i] = x_on[i] ? static_cast<uint32_t>(2 * ((m0 + tok) * a.sx + xk[i])) : 0u;
-    xs_off[i] = (j * BM + tok) * kXRow + 16 * x_chunk(tok, ch);
   }
   const int x_end = min(a.K, 64 * ce);
-  auto load_x = [&](int s, int i) {
-    const bool on = x_on[i] && xk[i] + 64 * KS * s < x_end;
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                         xrsrc, on ? xoff[i] + 2 * 64 * KS * s : kOutOfRange, 0, 0));
-  };
-  auto stage_x = [&](int buf, const u32x4* v) {
+  // Every wave issues XC loads per step, so the counts dma_barrier waits on
+  // are the same for all; a wave with no piece in range (XSPARE) writes the
+  // zeros its out-of-range loads return into the spare kilobyte.
+  auto load_x_lds = [&](int s) {
+    uint8_t* buf = xs + (s % kXBufs) * XBUF;
 #pragma unroll
     for (int i = 0; i < XC; ++i) {
-      if (XP % kGemmThreads == 0 || x_mine[i]) *reinterpret_cast<u32x4*>(&xs[buf][xs_off[i]]) = v[i];
+      const int qw = 64 * wave + kGemmThreads * i;  // the wave's first piece
+      uint8_t* dst = (!XSPARE || qw < XP) ? buf + 16 * qw : xs + kXBufs * XBUF;
+      const bool on = x_on[i] && xk[i] + 64 * KS * s < x_end;
+      buffer_load_lds16(xrsrc, dst, on ? xoff[i] + 2 * 64 * KS * s : kOutOfRange);
     }
   };
 
-  u32x4 wr[kPackRing][RW], xr[kPackRing][XC];
+  u32x4 wr[kPackRing][RW];
 #pragma unroll
   for (int r = 0; r < kPackRing; ++r) {
 #pragma unroll
     for (int j = 0; j < RW; ++j) wr[r][j] = load_w(r, j);
-#pragma unroll
-    for (int i = 0; i < XC; ++i) xr[r][i] = load_x(r, i);
   }
-  stage_x(0, xr[0]);
-  stage_x(1, xr[1]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int t = 0; t < kXLead; ++t) load_x_lds(t);
+  __builtin_amdgcn_sched_barrier(0);
 
   f32x4 acc[RW][CB];
 #pragma unroll
@@ -419,15 +474,19 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
     a0[j] = i8x8_to_operand<DT>(wr[0][j][0], wr[0][j][1]);
     a1[j] = i8x8_to_operand<DT>(wr[0][j][2], wr[0][j][3]);
   }
-  lds_barrier();
+  // x(0) and x(1) in LDS: the loads of x(2) .. x(kXLead - 1) may still be out.
+  dma_barrier<(kXLead - 2) * XC>();
 
   // One step s (ring slot r): read all of x(s) from LDS, refill slot r with
-  // step s + kPackRing, run the MFMAs on the weights converted last step,
-  // convert step s + 1's weights while they run, stage x(s + 2), and meet the
-  // other waves after odd steps (x(s + 2) goes to the buffer step s - 2 read,
-  // and every wave has passed the barrier after step s - 1).
-  auto step = [&](int s, bool refill, u32x4* wslot, u32x4* xslot, const u32x4* wnext, const u32x4* xnext) {
-    const uint8_t* xb = &xs[s & 3][xb_off];
+  // weights of step s + kPackRing, then load x(s + kXLead) into LDS, run the
+  // MFMAs on the weights converted last step, convert step s + 1's weights
+  // while they run, and meet the other waves after odd steps. At that barrier
+  // x(s + 1) and x(s + 2) must have landed: the loads issued after them are
+  // x(s + 3) .. x(s + kXLead) (XC each) and the weights of the steps since,
+  // counted here only for the steps of the current ring pass (NWAIT: a
+  // smaller count only waits longer).
+  auto step = [&](int s, bool refill, u32x4* wslot, const u32x4* wnext, auto nwait) {
+    const uint8_t* xb = xs + (s % kXBufs) * XBUF + xb_off;
     u32x4 b0[CB], b1[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
@@ -437,9 +496,9 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
     if (refill) {
 #pragma unroll
       for (int j = 0; j < RW; ++j) wslot[j] = load_w(s + kPackRing, j);
-#pragma unroll
-      for (int i = 0; i < XC; ++i) xslot[i] = load_x(s + kPackRing, i);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    load_x_lds(s + kXLead);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
@@ -454,24 +513,30 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
       a0[j] = i8x8_to_operand<DT>(wnext[j][0], wnext[j][1]);
       a1[j] = i8x8_to_operand<DT>(wnext[j][2], wnext[j][3]);
     }
-    stage_x((s + 2) & 3, xnext);
-    if (s & 1) lds_barrier();
+    if (s & 1) dma_barrier<decltype(nwait)::value>();
   };
+  // In a ring pass the odd steps r = 1, 3, 5 follow at least two refilling
+  // steps of the same pass; the last pass refills nothing.
+  static_assert(kXLead >= 4, "two refilling steps lie between x(s + 2) and an odd step's barrier");
+  using WaitRing = std::integral_constant<int, (kXLead - 2) * XC + 2 * RW>;
+  using WaitTail = std::integral_constant<int, (kXLead - 2) * XC>;
 
   int s0 = 0;
   for (; s0 + kPackRing <= steps; s0 += kPackRing) {
 #pragma unroll
-    for (int r = 0; r < kPackRing; ++r)
-      step(s0 + r, true, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 2) % kPackRing]);
+    for (int r = 0; r < kPackRing; ++r) step(s0 + r, true, wr[r], wr[(r + 1) % kPackRing], WaitRing{});
   }
 #pragma unroll
   for (int r = 0; r < kPackRing; ++r) {
-    if (s0 + r < steps) step(s0 + r, false, wr[r], xr[r], wr[(r + 1) % kPackRing], xr[(r + 2) % kPackRing]);
+    if (s0 + r < steps) step(s0 + r, false, wr[r], wr[(r + 1) % kPackRing], WaitTail{});
   }
-  if (steps & 1) lds_barrier();  // the last step read x: before LDS is reused below
+  // Every LDS load (those past the last step write zeros) lands before the
+  // wave goes on; before LDS is reused below, every wave's.
+  wait_vm<0>();
+  if constexpr (KS > 1) lds_barrier();
 
   if constexpr (KS > 1) {
-    f32x4* red = reinterpret_cast<f32x4*>(&xs[0][0]);  // [KS - 1][RB][RW][CB][64 lanes]
+    f32x4* red = reinterpret_cast<f32x4*>(xs);  // [KS - 1][RB][RW][CB][64 lanes]
     if (ks > 0) {
 #pragma unroll
       for (int j = 0; j < RW; ++j)
