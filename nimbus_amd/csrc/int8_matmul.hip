@@ -361,7 +361,7 @@ static int launch_gemm_dt(const GemmArgs& a, hipStream_t s) {
 // weights while they execute; the workgroup meets at a barrier every second
 // step.
 
-constexpr int kPackRing = 6;  // steps of weight loads in flight
+constexpr int kPackRing = 4;  // steps of weight loads in flight
 constexpr int kXBufs = 8;     // x steps in LDS
 constexpr int kXLead = kXBufs - 2;  // x loaded this many steps ahead
 
@@ -515,8 +515,10 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
     }
     if (s & 1) dma_barrier<decltype(nwait)::value>();
   };
-  // In a ring pass the odd steps r = 1, 3, 5 follow at least two refilling
-  // steps of the same pass; the last pass refills nothing.
+  // A ring pass starts on an even step, so its odd steps (r = 1, 3, ...)
+  // follow at least two refilling steps of the same pass; the last pass
+  // refills nothing.
+  static_assert(kPackRing % 2 == 0, "ring passes start on even steps");
   static_assert(kXLead >= 4, "two refilling steps lie between x(s + 2) and an odd step's barrier");
   using WaitRing = std::integral_constant<int, (kXLead - 2) * XC + 2 * RW>;
   using WaitTail = std::integral_constant<int, (kXLead - 2) * XC>;
