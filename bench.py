@@ -480,6 +480,7 @@ def time_mixed_step(batch, steps, warmup):
     from nimbus_amd import workloads
     from nimbus_amd.graphs import DecodeAttentionGraphs
     from nimbus_amd.kernels.cache_ops import write_kv
+    from nimbus_amd.kernels.paged_attention import paged_decode_attention
     from nimbus_amd.kernels.prefill_attention import build_programs, paged_prefill_attention
 
     nb = batch.k_cache.shape[0]
@@ -514,8 +515,30 @@ def time_mixed_step(batch, steps, warmup):
         w_us = _graph_us([write_all] * 32, steps, warmup)
     kvh, d = batch.k.shape[1], batch.k.shape[2]
     w_bytes = workloads.write_kv_bytes(int(batch.k.shape[0]), kvh, d, batch.k.element_size())
+    # The decode part apart from its tokens' slot write: the padded-64 decode call on the graphs' static
+    # buffers (max_context pinned at max_model_len, as captured), 16 calls back to back in a hipGraph; and the
+    # 64 slot writes alone the same way. Bytes: the 60 real decodes' algorithmic bytes (padding rows excluded).
+    dq, dctx, dbt = graphs.q[:gb], graphs.ctx[:gb], graphs.tables[:gb]
+    dout = torch.empty_like(dq)
+
+    def decode_only():
+        paged_decode_attention(dq, kc, vc, dctx, dbt, graphs.max_model_len, batch.scale, out=dout,
+                               workspace=graphs.workspace)
+
+    def decode_write():
+        write_kv(graphs.k[:gb], graphs.v[:gb], kc, vc, graphs.slots[:gb])
+
+    with torch.inference_mode():
+        d_us = _graph_us([decode_only] * 16, steps, warmup)
+        dw_us = _graph_us([decode_write] * 32, steps, warmup)
+    h = batch.q.shape[1]
+    d_bytes = workloads.decode_bytes(batch.decode_context_host(), h, kvh, d, batch.q.element_size())
     return {"step_us": statistics.mean(us), "decode_graph_replay_us": statistics.mean(replay_us),
             "padded_batch": gb, "tokens": int(batch.q.shape[0]),
+            "decode": {"bytes": d_bytes, "sum_ctx": int(sum(batch.decode_context_host())), "us_per_call_graph": d_us,
+                       "GBps": d_bytes / d_us / 1e3, "frac_hbm_peak": d_bytes / d_us / 1e3 / HBM_PEAK_GBS,
+                       "slot_write_us": dw_us,
+                       "replay_GBps": d_bytes / statistics.mean(replay_us) / 1e3},
             "write_kv": {"us_per_call": w_us, "bytes": w_bytes, "GBps": w_bytes / w_us / 1e3,
                          "frac_hbm_peak": w_bytes / w_us / 1e3 / HBM_PEAK_GBS}}
 
@@ -799,18 +822,32 @@ REFERENCE_PUBLISHED_US = {
     "paged_decode_attention batch=16 ctx=512": 98.3, "paged_decode_attention batch=64 ctx=512": 348.3,
     "paged_decode_attention batch=64 ctx=1024": 626.7, "paged_prefill_attention seqs=1 len=512": 118.9,
     "paged_prefill_attention seqs=4 len=512": 383.4, "paged_prefill_attention seqs=16 len=128": 203.4,
+    # results/kernels.json:72-176: add_rms_norm (fp16, hidden 2048) and the INT8 matmul (TinyLlama projections)
+    "add_rms_norm rows=1 hidden=2048": 10.0, "add_rms_norm rows=64 hidden=2048": 15.5,
+    "add_rms_norm rows=2048 hidden=2048": 273.0,
+    "int8_matmul qkv_proj M=1 N=2560 K=2048": 65.6, "int8_matmul qkv_proj M=16 N=2560 K=2048": 65.4,
+    "int8_matmul qkv_proj M=64 N=2560 K=2048": 73.8, "int8_matmul qkv_proj M=512 N=2560 K=2048": 358.6,
+    "int8_matmul gate_up_proj M=1 N=11264 K=2048": 239.7, "int8_matmul gate_up_proj M=16 N=11264 K=2048": 240.0,
+    "int8_matmul gate_up_proj M=64 N=11264 K=2048": 264.8, "int8_matmul gate_up_proj M=512 N=11264 K=2048": 1540.4,
+    "int8_matmul down_proj M=1 N=2048 K=5632": 126.6, "int8_matmul down_proj M=16 N=2048 K=5632": 128.6,
+    "int8_matmul down_proj M=64 N=2048 K=5632": 163.8, "int8_matmul down_proj M=512 N=2048 K=5632": 795.6,
 }
 
 
 def reference_shapes(reps=200, warmup=25):
-    """The shapes of the reference's kernel micro-bench (bench/kernels.py:54-74):
+    """The shapes of the reference's kernel micro-bench (bench/kernels.py:54-91):
     TinyLlama heads (H=32, KV=4, D=64), fp16, pages a seeded permutation of
     a pool of (pages needed + 8) blocks; decode at (batch, ctx) in {(1,512),
     (1,2048), (16,512), (64,512), (64,1024)}, fresh prefill of (seqs, len) in
-    {(1,512), (4,512), (16,128)}. Each call is timed alone between a HIP event
-    pair through the Python entry point (as triton.testing.do_bench does),
-    median of `reps`. The pools are at most 17 MB, so they sit in the Infinity
-    Cache: GB/s here is effective, not HBM."""
+    {(1,512), (4,512), (16,128)}; add_rms_norm of {1, 64, 2048} rows of 2048;
+    the INT8 matmul at TinyLlama's qkv (2560 x 2048), gate_up (11264 x 2048)
+    and down (2048 x 5632) projections for M in {1, 16, 64, 512}, on the
+    tile-order weights Int8Linear keeps, beside torch's fp16 matmul of the
+    dequantized weights (the reference's cuBLAS column). Each call is timed
+    alone between a HIP event pair through the Python entry point (as
+    triton.testing.do_bench does), median of `reps`. The inputs are at most
+    a few tens of MB, so they sit in the Infinity Cache: GB/s here is
+    effective, not HBM."""
     import torch
 
     from nimbus_amd import workloads
@@ -848,6 +885,37 @@ def reference_shapes(reps=200, warmup=25):
         rows.append({"kernel": name, "us": us, "TFLOPs": flops / us / 1e6,
                      "frac_mfma_peak": flops / us / 1e6 / MFMA_BF16_PEAK_TFLOPS,
                      "reference_published_us": REFERENCE_PUBLISHED_US[name]})
+    from nimbus_amd.kernels.int8_matmul import int8_matmul_packed, pack_int8_weight
+    from nimbus_amd.kernels.rmsnorm import add_rms_norm
+    from nimbus_amd.quant import dequantize_weight, quantize_weight
+
+    def median_us(fn):
+        for i in range(warmup):
+            fn(i)
+        return statistics.median(event_times_us(fn, reps, stream))
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for m in (1, 64, 2048):
+        x = torch.randn(m, 2048, generator=g, device="cuda").half()
+        r = torch.randn(m, 2048, generator=g, device="cuda").half()
+        w = torch.randn(2048, generator=g, device="cuda").half()
+        us = median_us(lambda i: add_rms_norm(x, r, w, 1e-5))
+        nbytes = 4 * m * 2048 * 2 + 2048 * 2
+        name = f"add_rms_norm rows={m} hidden=2048"
+        rows.append({"kernel": name, "us": us, "GBps_effective": nbytes / us / 1e3,
+                     "reference_published_us": REFERENCE_PUBLISHED_US[name]})
+    for proj, n, k in (("qkv_proj", 2560, 2048), ("gate_up_proj", 11264, 2048), ("down_proj", 2048, 5632)):
+        wq, sc = quantize_weight(torch.randn(n, k, generator=g, device="cuda").half() * 0.02)
+        packed = pack_int8_weight(wq)
+        dense = dequantize_weight(wq, sc)
+        for m in (1, 16, 64, 512):
+            x = torch.randn(m, k, generator=g, device="cuda").half()
+            us = median_us(lambda i: int8_matmul_packed(x, packed, sc, n, k))
+            dense_us = median_us(lambda i: torch.matmul(x, dense.T))
+            nbytes = n * k + 2 * m * k + 2 * m * n + 2 * n
+            name = f"int8_matmul {proj} M={m} N={n} K={k}"
+            rows.append({"kernel": name, "us": us, "GBps_effective": nbytes / us / 1e3,
+                         "torch_fp16_matmul_us": dense_us, "reference_published_us": REFERENCE_PUBLISHED_US[name]})
     return {"note": "reference_published_us: the reference's Triton kernels on an RTX 4050 Laptop GPU "
                     "(results/kernels.json), other hardware", "rows": rows}
 
@@ -929,6 +997,39 @@ def all_configs(steps, warmup, out_path=None):
 
 
 # ---------------------------------------------------------------- main
+
+def config_summary(result):
+    """One compact entry per BASELINE config: µs per call and the roofline
+    fraction (HBM for decode, dense MFMA for prefill)."""
+    def r4(x):
+        return None if x is None else round(float(x), 4)
+
+    out = {}
+    other = result.get("other_configs") or {}
+    c1 = other.get("config1")
+    if c1:
+        out["config1_decode"] = {"us_graph": r4(c1["us_per_call_graph"]), "us_eager": r4(c1["us_per_call"]),
+                                 "frac_hbm": r4(c1["bytes"] / c1["us_per_call_graph"] / 1e3 / HBM_PEAK_GBS)}
+    c2 = other.get("config2")
+    if c2:
+        out["config2_prefill"] = {"us": r4(c2["us_per_call"]), "frac_mfma": r4(c2["frac_mfma_peak"])}
+    rl = result["roofline"]
+    out["config3_decode"] = {"us": r4(rl["kernel_us"]), "us_graph": r4(rl["kernel_us_graph"]), "frac_hbm": r4(rl["frac"])}
+    if "prefill" in result:
+        out["config4_prefill"] = {"us": r4(result["prefill"]["us_per_call"]),
+                                  "frac_mfma": r4(result["prefill"]["frac_mfma_peak"])}
+    ms = result.get("mixed_step")
+    if ms:
+        out["config4_decode"] = {"us_graph": r4(ms["decode"]["us_per_call_graph"]),
+                                 "frac_hbm": r4(ms["decode"]["frac_hbm_peak"]),
+                                 "slot_write_us": r4(ms["decode"]["slot_write_us"]),
+                                 "step_us": r4(ms["step_us"])}
+    c5 = other.get("config5")
+    if c5:
+        out["config5_decode"] = {"us": r4(c5["us_per_call"]), "us_graph": r4(c5["us_per_call_graph"]),
+                                 "frac_hbm": r4(c5["frac_hbm_peak_call"])}
+    return out
+
 
 def main(argv=None):
     args = parse(argv)
@@ -1049,7 +1150,12 @@ def main(argv=None):
             del long_b
             torch.cuda.empty_cache()
         result["cpu_baseline"] = dict(base, entries=entries)
+    # Last on the line (and repeated on stderr after it), where a reader of the output's tail finds it: one
+    # figure per BASELINE config and its share of the roofline.
+    result["summary"] = summary = config_summary(result)
     print(json.dumps(result), flush=True)
+    for k, v in summary.items():
+        log(f"summary {k}: {v}")
 
 
 if __name__ == "__main__":

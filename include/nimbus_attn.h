@@ -244,7 +244,9 @@ int nimbus_paged_verify(int32_t queries_per_seq, const void* q, int64_t q_stride
  * masked block takes any row: the chunked kernel when cols is a multiple of
  * 8 and at most 8192, every pointer 16-byte aligned and every row stride a
  * multiple of 8; otherwise a general kernel (an element per thread, for rows
- * no Llama layer has).
+ * no Llama layer has). residual_out may alias x or residual (an in-place
+ * residual update): every element is read before it is written, by the
+ * thread that writes it. out must not overlap x, residual or residual_out.
  */
 int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
                         const void* weight, void* out, int64_t out_stride, void* residual_out,

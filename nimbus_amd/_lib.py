@@ -139,6 +139,8 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 def stream_of(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    """The raw handle of the current stream on t's device (the capture stream
+    inside torch.cuda.graph), read without building a Stream object."""
+    return torch._C._cuda_getCurrentRawStream(t.get_device())
 
 

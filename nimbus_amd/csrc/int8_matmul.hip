@@ -104,12 +104,13 @@ __device__ __forceinline__ u32x4 i8x8_to_operand<kFloat16>(uint32_t w0, uint32_t
 // v_cvt_f32_i32 whose SDWA operand select picks and extends the byte), and
 // the upper half of that fp32 is the byte's bf16, exactly (|b| <= 128 needs
 // at most 8 significant bits). Six VALU ops per four weights.
+// (The byte is moved to the top in unsigned arithmetic, then shifted back
+// down arithmetically: a left shift of a negative int32 is undefined.)
 __device__ __forceinline__ u32x2 i8x4_to_bf16x4(uint32_t w) {
-  const int32_t s = static_cast<int32_t>(w);
-  const float f0 = static_cast<float>((s << 24) >> 24);
-  const float f1 = static_cast<float>((s << 16) >> 24);
-  const float f2 = static_cast<float>((s << 8) >> 24);
-  const float f3 = static_cast<float>(s >> 24);
+  const float f0 = static_cast<float>(static_cast<int32_t>(w << 24) >> 24);
+  const float f1 = static_cast<float>(static_cast<int32_t>(w << 16) >> 24);
+  const float f2 = static_cast<float>(static_cast<int32_t>(w << 8) >> 24);
+  const float f3 = static_cast<float>(static_cast<int32_t>(w) >> 24);
   // upper halves of (f0, f1) and (f2, f3)
   return u32x2{__builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u),
                __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u)};

@@ -195,8 +195,11 @@ static int launch_norm(const NormArgs& a, hipStream_t s) {
 // past 8192, rows off their 16-byte alignment), as the Triton kernel's
 // masked block takes any row. One 256-thread workgroup per row at a time,
 // an element per thread per pass: the sum of squares of the rounded sums,
-// reduced as above, then a second pass that forms the sum again (it does not
-// read back what the first pass stored) and writes the output.
+// reduced as above, then a second pass that writes the output. With a
+// residual, the second pass reads back the rounded sum the first pass stored
+// in residual_out (the same thread wrote it): residual_out may then alias x
+// or the residual, as it may in the chunked kernel, since every element is
+// read before it is written and by the thread that writes it.
 template <int DT>
 __device__ __forceinline__ float elem_f32(uint16_t v) {
   return Elem<DT>::to_f32(v);
@@ -227,7 +230,10 @@ __global__ __launch_bounds__(256) void add_rms_norm_general_kernel(NormArgs a) {
     par ^= 1;
     const float inv = 1.f / __builtin_sqrtf(ss / static_cast<float>(a.cols) + a.eps);
     for (int c = threadIdx.x; c < a.cols; c += 256) {
-      const float y = elem_f32<DT>(Elem<DT>::from_f32(sum_at(row, c) * inv));  // dtype(s * rsqrt(...))
+      float v;
+      if constexpr (RES) v = elem_f32<DT>(a.rout[static_cast<int64_t>(row) * a.sro + c]);
+      else v = sum_at(row, c);
+      const float y = elem_f32<DT>(Elem<DT>::from_f32(v * inv));  // dtype(s * rsqrt(...))
       a.out[static_cast<int64_t>(row) * a.so + c] = Elem<DT>::from_f32(elem_f32<DT>(a.w[c]) * y);
     }
   }

@@ -406,6 +406,12 @@ class DecodeGraphs:
         for i, s in enumerate(seqs):
             tables[i, :widths[i]] = s.block_table
         pos = np.fromiter((s.num_computed for s in seqs), dtype=np.int64, count=n)
+        short = np.flatnonzero(pos // bs >= np.asarray(widths, dtype=np.int64))
+        if short.size:
+            # (the zero padding past a table's width would send the token's K/V to block 0, which another
+            # sequence may own; nimbus/cuda_graph.py:118-135 raises IndexError on block_table[p // bs])
+            i = int(short[0])
+            raise IndexError(f"sequence {i} has {widths[i]} blocks, too few for position {int(pos[i])}")
         rows[0, :n] = [s.token_ids[p] for s, p in zip(seqs, pos.tolist())]
         rows[1, :n] = pos
         rows[2, :n] = tables[np.arange(n), pos // bs].astype(np.int64) * bs + pos % bs
@@ -542,6 +548,13 @@ class VerifyGraphs:
             ctx[i] = len(s)
             rows[0, i * q:(i + 1) * q] = s.token_ids[len(s) - q:]
         pos = (ctx[:n, None].astype(np.int64) - q + np.arange(q)[None, :]).reshape(-1)
+        widths = np.repeat(np.fromiter((len(s.block_table) for s in seqs), dtype=np.int64, count=n), q)
+        short = np.flatnonzero(pos // bs >= widths)
+        if short.size:
+            # (as DecodeGraphs._load: nimbus/spec/engine.py:117-128 raises IndexError on block_table[p // bs])
+            i = int(short[0]) // q
+            raise IndexError(f"sequence {i} has {len(seqs[i].block_table)} blocks, too few for position "
+                             f"{int(pos[short[0]])}")
         rows[1, :n * q] = pos
         rows[2, :n * q] = tables[np.repeat(np.arange(n), q), pos // bs].astype(np.int64) * bs + pos % bs
         pad = np.arange(q, dtype=np.int64)

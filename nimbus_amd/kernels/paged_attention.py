@@ -27,6 +27,19 @@ def decode_workspace_bytes(batch: int, heads: int, head_dim: int, max_context: i
     return int(_lib.load().nimbus_paged_decode_workspace_bytes(batch, heads, head_dim, max_context))
 
 
+# Workspace sizes by (batch, heads, head dim, max_context): a pure function of
+# the shape, asked once per shape instead of once per call.
+_WS_BYTES: dict[tuple[int, int, int, int], int] = {}
+
+
+def _decode_ws_bytes(lib, b: int, h: int, d: int, max_context: int) -> int:
+    key = (b, h, d, max_context)
+    n = _WS_BYTES.get(key)
+    if n is None:
+        n = _WS_BYTES[key] = int(lib.nimbus_paged_decode_workspace_bytes(b, h, d, max_context))
+    return n
+
+
 # Workspaces cached per (device, stream), grown on demand, so a call does not
 # allocate. Buffers that were outgrown stay alive: a captured graph may still
 # use them.
@@ -41,7 +54,7 @@ def new_decode_workspace(nbytes: int, device) -> torch.Tensor:
 
 def _cached_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     index = device.index if device.index is not None else torch.cuda.current_device()
-    key = (index, torch.cuda.current_stream(device).cuda_stream)
+    key = (index, torch._C._cuda_getCurrentRawStream(index))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
@@ -54,9 +67,10 @@ def _cached_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
 def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
     if k_cache.dim() != 4 or k_cache.shape != v_cache.shape:
         raise ValueError("k_cache and v_cache must both be [num_blocks, block_size, KV, D]")
-    if k_cache.stride() != v_cache.stride():
+    kst = k_cache.stride()
+    if kst != v_cache.stride():
         raise ValueError("v_cache must share k_cache's strides")
-    if k_cache.stride(-1) != 1:
+    if kst[3] != 1:
         raise ValueError("caches need unit stride in the head dim")
     if k_cache.dtype != v_cache.dtype:
         raise ValueError("k_cache and v_cache must share one dtype")
@@ -122,19 +136,20 @@ def paged_decode_attention(
     if index_checks.enabled():
         index_checks.check_tables(block_tables, context_lens, k_cache.shape[0], k_cache.shape[1])
     lib = _lib.load()
-    need = lib.nimbus_paged_decode_workspace_bytes(b, h, d, int(max_context))
+    max_context = int(max_context)
+    need = _decode_ws_bytes(lib, b, h, d, max_context)
     if workspace is not None:
         if workspace.numel() * workspace.element_size() < need or not workspace.is_cuda:
             raise ValueError(f"workspace smaller than the {need} bytes this call needs")
         ws = workspace
     else:
         ws = _cached_workspace(need, q.device)
+    qst, cst, ost = q.stride(), k_cache.stride(), out.stride()
     rc = getattr(lib, _entry)(
-        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0],
-        k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), block_tables.data_ptr(), block_tables.stride(0),
-        block_tables.shape[1], context_lens.data_ptr(), out.data_ptr(), out.stride(0), out.stride(1),
-        ws.data_ptr(), ws.numel() * ws.element_size(), b, h, kv, d, k_cache.shape[1], int(max_context), float(scale),
-        _lib.dtype_code(q.dtype), _lib.stream_of(q))
+        q.data_ptr(), qst[0], qst[1], k_cache.data_ptr(), v_cache.data_ptr(), k_cache.shape[0], cst[0], cst[1],
+        cst[2], block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1], context_lens.data_ptr(),
+        out.data_ptr(), ost[0], ost[1], ws.data_ptr(), ws.nbytes, b, h, kv, d, k_cache.shape[1], max_context,
+        float(scale), _lib.dtype_code(q.dtype), _lib.stream_of(q))
     _lib.check(rc, _entry)
     return out
 

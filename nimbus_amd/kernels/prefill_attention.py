@@ -98,8 +98,25 @@ def build_programs(query_start_host: list[int], device,
             half = (order.size + 1) // 2
             order = np.concatenate([order[:half], order[half:][::-1]])
         seqs, starts = seqs[order], starts[order]
-    t = torch.from_numpy(np.stack([seqs, starts]).astype(np.int32)).to(device, non_blocking=True)
+    t = _to_device(np.stack([seqs, starts]).astype(np.int32), device)
     return t[0], t[1]
+
+
+def _to_device(arr: np.ndarray, device) -> torch.Tensor:
+    """arr on the device through pinned host memory (an asynchronous copy;
+    torch's pinned-memory cache keeps the host block until the copy is done).
+    A copy from pageable memory would wait for the host-side staging."""
+    if torch.device(device).type != "cuda":
+        return torch.from_numpy(arr).to(device)
+    host = torch.empty(arr.shape, dtype=torch.from_numpy(arr[:0]).dtype, pin_memory=True)
+    host.numpy()[...] = arr
+    return host.to(device, non_blocking=True)
+
+
+# The last tile table built for a call without one: (key, table). Eager callers
+# that pass programs=None with the same host lists (every layer of a step)
+# reuse it instead of building and copying it again.
+_LAST_TABLE: list = [None, None]
 
 
 KEY_BLOCK = 64  # keys per block of the prefill kernel's walk
@@ -169,8 +186,8 @@ def plan_pieces(query_start_host: list[int], context_lens_host: list[int], num_h
         slot += k
     rows.sort(key=lambda r: -r[0])
     table = np.asarray([r[1:] for r in rows], dtype=np.int32)
-    t = torch.from_numpy(table).to(device, non_blocking=True)
-    mt = torch.from_numpy(np.asarray(merges, dtype=np.int32).reshape(-1, 4)).to(device, non_blocking=True)
+    t = _to_device(table, device)
+    mt = _to_device(np.asarray(merges, dtype=np.int32).reshape(-1, 4), device)
     return PrefillPieces(t, mt, slot)
 
 
@@ -241,7 +258,11 @@ def paged_prefill_attention(
     if index_checks.enabled():
         index_checks.check_tables(block_tables, context_lens, k_cache.shape[0], k_cache.shape[1])
     if programs is None:
-        programs = build_programs(query_start_host, q.device, context_lens_host)
+        key = (q.device, tuple(query_start_host), tuple(context_lens_host))
+        if _LAST_TABLE[0] != key or torch.cuda.is_current_stream_capturing():
+            _LAST_TABLE[1] = build_programs(query_start_host, q.device, context_lens_host)
+            _LAST_TABLE[0] = key
+        programs = _LAST_TABLE[1]
     if q.stride(-1) != 1:
         q = q.contiguous()
     if block_tables.stride(1) != 1:

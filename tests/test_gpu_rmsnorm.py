@@ -155,3 +155,27 @@ def test_unaligned_rows_take_the_general_kernel():
     assert torch.equal(_bits(got_r.cpu()), _bits(want_r)) and torch.equal(got_r, al_r)
     assert_norm_close(got_y.cpu(), want_y)
     torch.testing.assert_close(got_y, al_y, atol=4e-3, rtol=2e-3)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("cols", [777, 16384, 4096])
+@pytest.mark.parametrize("alias", ["residual", "x"])
+def test_residual_out_may_alias_an_input(dtype, cols, alias):
+    """Through the C ABI with residual_out the very buffer of the residual
+    (or of x): an in-place residual update. The general kernel (777, 16384
+    columns) and the chunked one (4096) give the oracle's new residual bit
+    for bit and its output to the bar."""
+    from nimbus_amd import _lib
+
+    announce(f"add_rms_norm residual_out aliasing {alias} dtype={dtype} cols={cols}")
+    x, r, w = _inputs(5, cols, dtype, cols + 3)
+    want_y, want_r = reference.add_rms_norm(x.cpu(), r.cpu(), w.cpu(), 1e-5)
+    out = torch.empty_like(x)
+    dst = r if alias == "residual" else x
+    rc = _lib.load().nimbus_add_rms_norm(x.data_ptr(), x.stride(0), r.data_ptr(), r.stride(0), w.data_ptr(),
+                                         out.data_ptr(), out.stride(0), dst.data_ptr(), dst.stride(0), x.shape[0],
+                                         cols, 1e-5, _lib.dtype_code(dtype), _lib.stream_of(x))
+    _lib.check(rc, "nimbus_add_rms_norm")
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(dst.cpu()), _bits(want_r))
+    assert_norm_close(out.cpu(), want_y)

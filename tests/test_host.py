@@ -326,3 +326,39 @@ def test_index_checks_raise_like_the_reference():
         index_checks.check_tables(torch.tensor([[-2]], dtype=torch.int32), torch.tensor([1], dtype=torch.int32),
                                   4, 16)
     assert not index_checks.enabled() or os.environ.get("NIMBUS_CHECK_INDICES")
+
+
+def _bare_loader(cls, max_batch=8, width=4, q_len=None):
+    """A graph set's host-side loader state alone (plain host buffers, no
+    capture): enough to run _load's checks, which come before any copy."""
+    from nimbus_amd import graphs
+
+    g = object.__new__(getattr(graphs, cls))
+    g.block_size, g.max_batch, g.scratch_block = 16, max_batch, 99
+    g.scratch_slot = 99 * 16
+    g.sizes = [1, 2, 4, 8]
+    g._staged = None
+    rows = 4 if q_len is None else 3
+    g._host = torch.zeros((rows, max_batch * (q_len or 1)), dtype=torch.int64)
+    g._host_tables = torch.zeros((max_batch, width), dtype=torch.int32)
+    if q_len is not None:
+        g.q_len = q_len
+        g._host_ctx = torch.zeros(max_batch, dtype=torch.int32)
+    return g
+
+
+def test_decode_graph_loader_refuses_a_short_block_table():
+    # Position 32 needs a third block; the table holds two. The zero padding past
+    # it must not become block 0 (nimbus/cuda_graph.py:118-135 raises IndexError).
+    g = _bare_loader("DecodeGraphs")
+    seqs = [workloads.SeqState(list(range(10)), [5], 9), workloads.SeqState(list(range(33)), [3, 4], 32)]
+    with pytest.raises(IndexError, match="sequence 1"):
+        g._load(seqs)
+
+
+def test_verify_graph_loader_refuses_a_short_block_table():
+    # The last of 5 fed tokens of sequence 1 sits at position 16: a second block is needed.
+    g = _bare_loader("VerifyGraphs", q_len=5)
+    seqs = [workloads.SeqState(list(range(9)), [1]), workloads.SeqState(list(range(17)), [2])]
+    with pytest.raises(IndexError, match="sequence 1"):
+        g._load(seqs, 2)
