@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 11
+#define NIMBUS_ATTN_ABI_VERSION 12
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -197,6 +197,43 @@ int nimbus_paged_prefill_pieces(const void* q, int64_t q_stride_t, int64_t q_str
                                 int64_t workspace_bytes, void* out, int64_t out_stride_t, int64_t out_stride_h,
                                 int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
                                 float scale, int32_t dtype, void* stream);
+
+/*
+ * nimbus_paged_prefill with the batch's work balanced over the workgroups
+ * the chip holds at once (stream-K), for any batch. Per kv-head group, the
+ * 64-key blocks of every unit (NIMBUS_PREFILL_TILE / 2 positions of 4 query
+ * heads, or the kernel's 128 rows at other GQA ratios) are laid end to end
+ * and cut into num_shares contiguous shares; workgroup (share j, kv-head
+ * group g) is grid index j * groups + g, and num_shares * groups must not
+ * exceed twice the device's CU count (NIMBUS_ERR_UNSUPPORTED otherwise).
+ * share_start [num_shares + 1] and pieces [n][8] int32 are the host's plan:
+ * share j walks pieces[share_start[j] .. share_start[j+1]) in order, each
+ * (sequence, first query of the unit, first key block, end key block
+ * (INT32_MAX: the unit's causal end), slot, fix_lo, fix_hi, 0). slot >= 0:
+ * the piece's fp32 (O, m, l) go to share slot `slot` of its kv-head group
+ * for a later share to fold in; slot -1: the piece finishes its unit,
+ * first folding in the pieces of shares [fix_lo, fix_hi), which must be
+ * lower than its own (it waits for each to be written), and writes out.
+ * Workspace: nimbus_paged_prefill_stream_workspace_bytes(); its first
+ * nimbus_paged_prefill_stream_flag_bytes() must be zero before the first
+ * call (flags, then an error word), and a completed call leaves them zero
+ * (the error word aside, which turns nonzero if a wait ever gives up on an
+ * inconsistent plan). Calls sharing a workspace must not overlap.
+ * Replaces the same reference interface as nimbus_paged_prefill
+ * (nimbus/kernels/prefill_attention.py:93-119); the plan stands in for the
+ * tile table of build_programs (prefill_attention.py:81-90).
+ */
+int64_t nimbus_paged_prefill_stream_flag_bytes(int32_t num_shares, int32_t num_heads, int32_t num_kv_heads);
+int64_t nimbus_paged_prefill_stream_workspace_bytes(int32_t num_shares, int32_t num_heads, int32_t num_kv_heads,
+                                                    int32_t head_dim);
+int nimbus_paged_prefill_stream(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_cache,
+                                const void* v_cache, int64_t num_blocks, int64_t cache_stride_block,
+                                int64_t cache_stride_token, int64_t cache_stride_head, const int32_t* block_tables,
+                                int64_t bt_stride, int32_t bt_width, const int32_t* query_start,
+                                const int32_t* context_lens, const int32_t* share_start, const int32_t* pieces,
+                                int32_t num_shares, void* workspace, int64_t workspace_bytes, void* out,
+                                int64_t out_stride_t, int64_t out_stride_h, int32_t num_heads, int32_t num_kv_heads,
+                                int32_t head_dim, int32_t block_size, float scale, int32_t dtype, void* stream);
 
 /*
  * Bytes of workspace nimbus_paged_verify needs (as for the decode workspace,

@@ -27,7 +27,7 @@ NIMBUS_ERR_ALIGNMENT = -3
 NIMBUS_ERR_WORKSPACE = -4
 NIMBUS_ERR_SCRATCH = -5
 NOALLOC_SCRATCH_BYTES = 64 << 20  # NIMBUS_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 # Entry points and their C signatures, in the order include/nimbus_attn.h declares them.
 _c_int, _c_i32, _c_i64, _c_p, _c_f = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
@@ -53,6 +53,11 @@ SIGNATURES = {
                                              _c_i64, _c_i32, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_i32, _c_i32, _c_p,
                                              _c_i64, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f,
                                              _c_i32, _c_p]),
+    "nimbus_paged_prefill_stream_flag_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32]),
+    "nimbus_paged_prefill_stream_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
+    "nimbus_paged_prefill_stream": (_c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_p,
+                                             _c_i64, _c_i32, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_p, _c_i64, _c_p,
+                                             _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f, _c_i32, _c_p]),
     "nimbus_paged_verify_workspace_bytes": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i64]),
     "nimbus_paged_verify": None,
     "nimbus_add_rms_norm": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i32,

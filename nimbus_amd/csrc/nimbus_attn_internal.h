@@ -7,4 +7,8 @@ namespace nimbus {
 
 constexpr int kPrefillTile = NIMBUS_PREFILL_TILE;          // query positions per tile-table entry
 
+// CU count of the current device (asked of the runtime once per device);
+// 0 or a hipError_t.
+int device_cus(int64_t* cus);
+
 }  // namespace nimbus

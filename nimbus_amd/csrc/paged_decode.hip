@@ -690,7 +690,7 @@ static int64_t waves_per_group(int64_t cus, int kvg, int64_t max_pages) {
 constexpr int kMaxDevices = 64;
 static std::atomic<int> g_device_cus[kMaxDevices];  // 0: not asked yet
 
-static int device_cus(int64_t* cus) {
+int device_cus(int64_t* cus) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return static_cast<int>(e);

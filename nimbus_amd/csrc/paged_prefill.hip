@@ -77,6 +77,17 @@ struct PrefillArgs {
   int64_t o_st, o_sh;
   int32_t H, G, gsplit, kvg;
   float scale_log2;
+  // Stream-K plan (nimbus_paged_prefill_stream), null otherwise: the pieces
+  // of share j are sk_piece[sk_start[j] .. sk_start[j + 1]), kSkFields int32
+  // each; sk_part holds the split pieces' (O, m, l) per (share, kv-head group,
+  // wave); sk_flag one word per (share, kv-head group, wave), 1 while that
+  // slot holds a piece not yet folded in; sk_err is set when a wait gives up.
+  const int32_t* sk_start;
+  const int32_t* sk_piece;
+  float* sk_part;
+  int32_t* sk_flag;
+  int32_t* sk_err;
+  int32_t sk_shares;  // shares per kv-head group (the grid is sk_shares * kvg)
 };
 
 template <int GS>
@@ -157,8 +168,26 @@ using IntC = std::integral_constant<int, N>;
 template <bool B>
 using BoolC = std::integral_constant<bool, B>;
 
-template <int DT, int D, int GS>
-__device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
+// Stream-K plan (nimbus_paged_prefill_stream): piece record fields.
+enum SkField : int { kSkSeq = 0, kSkM0, kSkKb0, kSkKb1, kSkSlot, kSkFixLo, kSkFixHi, kSkFields = 8 };
+// Polls of a fix-up wait before it gives up and flags the call as failed
+// (the contributors it waits on are lower-numbered workgroups, dispatched
+// before it, so a wait ends unless the plan is inconsistent).
+constexpr int kSkMaxPolls = 1 << 22;
+
+// SK: the workgroup walks the pieces of its stream-K share (one kv-head
+// group, the share's list of (unit, key-block range) pieces); otherwise it
+// is one unit of the tile table or of a key-range piece table.
+// The kernel's argument block, read through the kernel-argument segment
+// (the kernels' only argument sits at its start).
+typedef const __attribute__((address_space(4))) PrefillArgs* ArgsPtr;
+__device__ __forceinline__ ArgsPtr kernel_args() {
+  return (ArgsPtr)(__builtin_amdgcn_kernarg_segment_ptr());
+}
+
+template <int DT, int D, int GS, bool SK>
+__device__ __forceinline__ void prefill_unit() {
+  ArgsPtr a_top = kernel_args();
   using Shape = PrefillShape<GS>;
   constexpr int NT = Shape::kThreads;
   constexpr int POS = Shape::kPos;
@@ -173,13 +202,28 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   __shared__ __attribute__((aligned(16))) uint16_t ks[2 * TILE];
   __shared__ __attribute__((aligned(16))) uint16_t vs[2 * TILE];
 
-  // Unit: kv-head group fastest, then the sub-tile, then the table entry.
-  const int kvg_id = blockIdx.x % a.kvg;
-  const int r_unit = blockIdx.x / a.kvg;
-  const int entry = r_unit / Shape::kSub;
-  const int sub = r_unit % Shape::kSub;
-  const int kvh = kvg_id / a.gsplit;
-  const int gsub = kvg_id % a.gsplit;
+  // Unit: kv-head group fastest, then the sub-tile, then the table entry
+  // (stream-K: kv-head group fastest, then the share).
+  const int kvg_id = blockIdx.x % a_top->kvg;
+  const int r_unit = blockIdx.x / a_top->kvg;
+  const int kvh = kvg_id / a_top->gsplit;
+  const int gsub = kvg_id % a_top->gsplit;
+
+  int p_first = 0, p_end = 1;
+  if constexpr (SK) {
+    p_first = scalar_load_i32(a_top->sk_start, r_unit);
+    p_end = scalar_load_i32(a_top->sk_start, r_unit + 1);
+  }
+  for (int pc = p_first; pc < p_end; ++pc) {
+  // Stream-K reads the arguments again for each piece (through a pointer the
+  // compiler cannot see through): kept in scalar registers across the walk,
+  // they would crowd out the walk's own.
+  ArgsPtr ap = kernel_args();
+  if constexpr (SK) {
+    asm volatile("" : "+s"(ap));
+    if (pc > p_first) __syncthreads();  // the previous piece's last LDS reads are done
+  }
+  const auto& a = *ap;
   // The unit's record (sequence, first query, key blocks [kb0, kb1), piece
   // slot), read without a branch: the plain tile table takes its block range
   // and slot from kWholeUnit. Before the first K/V copy the workgroup then
@@ -192,15 +236,30 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // issues that round's loads together and none of them later)
   asm volatile("" ::"s"(a.pieces), "s"(a.prog_seq), "s"(a.prog_m), "s"(a.bt), "s"(a.bt_sb), "s"(a.qstart),
                "s"(a.ctx), "s"(a.q), "s"(a.kc), "s"(a.vc), "s"(a.c_sb), "s"(a.c_st), "s"(a.c_sh));
-  const int32_t* p_rec = a.pieces ? a.pieces + 5 * entry : a.prog_seq + entry;
-  const int32_t* p_m = a.pieces ? p_rec + 1 : a.prog_m + entry;
-  const int32_t* p_blk = a.pieces ? p_rec + 2 : kWholeUnit;
-  int seq = scalar_load_i32(p_rec, 0);
-  int m_entry = scalar_load_i32(p_m, 0);
-  int kb0 = scalar_load_i32(p_blk, 0);
-  int kb1 = scalar_load_i32(p_blk, 1);
-  int slot = scalar_load_i32(p_blk, 2);
-  asm volatile("" : "+s"(seq), "+s"(m_entry), "+s"(kb0), "+s"(kb1), "+s"(slot));
+  int seq, m_entry, kb0, kb1, slot, fix_lo = 0, fix_hi = 0;
+  const int entry = r_unit / Shape::kSub;
+  const int sub = r_unit % Shape::kSub;
+  if constexpr (SK) {
+    const int32_t* rec = a.sk_piece + kSkFields * pc;
+    seq = scalar_load_i32(rec, kSkSeq);
+    m_entry = scalar_load_i32(rec, kSkM0);
+    kb0 = scalar_load_i32(rec, kSkKb0);
+    kb1 = scalar_load_i32(rec, kSkKb1);
+    slot = scalar_load_i32(rec, kSkSlot);
+    fix_lo = scalar_load_i32(rec, kSkFixLo);
+    fix_hi = scalar_load_i32(rec, kSkFixHi);
+    asm volatile("" : "+s"(seq), "+s"(m_entry), "+s"(kb0), "+s"(kb1), "+s"(slot), "+s"(fix_lo), "+s"(fix_hi));
+  } else {
+    const int32_t* p_rec = a.pieces ? a.pieces + 5 * entry : a.prog_seq + entry;
+    const int32_t* p_m = a.pieces ? p_rec + 1 : a.prog_m + entry;
+    const int32_t* p_blk = a.pieces ? p_rec + 2 : kWholeUnit;
+    seq = scalar_load_i32(p_rec, 0);
+    m_entry = scalar_load_i32(p_m, 0);
+    kb0 = scalar_load_i32(p_blk, 0);
+    kb1 = scalar_load_i32(p_blk, 1);
+    slot = scalar_load_i32(p_blk, 2);
+    asm volatile("" : "+s"(seq), "+s"(m_entry), "+s"(kb0), "+s"(kb1), "+s"(slot));
+  }
   kb0 = max(kb0, 0);  // (a piece's first block; the page ids below are indexed from it)
   const int32_t* btrow = a.bt + seq * a.bt_sb;
   const int page_cap = a.bt_width - 1;
@@ -230,9 +289,12 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   pg_first = checked(pg_first);
   pg_v = checked(pg_v);
   pg_k = checked(pg_k);
-  const int m0 = m_entry + sub * POS;
+  const int m0 = SK ? m_entry : m_entry + sub * POS;
   const int q_len = qe - qs;
-  if (m0 >= q_len) return;  // the whole workgroup: this sub-tile has no queries
+  if (m0 >= q_len) {  // the whole workgroup: this sub-tile has no queries (nor has it for any other piece of it)
+    if constexpr (SK) continue;
+    else return;
+  }
   const int ctx = min(ctx_in, a.bt_width * 16);
   const int base_pos = ctx - q_len;  // absolute position of query 0
   const int kv_end = max(0, min(ctx, base_pos + m0 + POS));
@@ -241,7 +303,15 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   const int kbeg = min(kb0, n_kb_all);
   const int kend = min(kb1, n_kb_all);
 
-  const int tid = threadIdx.x;
+  int tid = threadIdx.x;
+  if constexpr (SK) {
+    // (formed again for each piece from the lane count and a wave index the
+    // compiler cannot see through, so that the lane-dependent offsets below
+    // are not kept live across all the pieces)
+    int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    asm volatile("" : "+s"(w));
+    tid = 64 * w + __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  }
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64) & (Shape::kWaves - 1);  // scalar, range known
   const int lane = tid % 64;
   const int col = lane % 32;  // this lane's row of the wave's 32
@@ -266,7 +336,6 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) qop[kk] = *reinterpret_cast<const u32x4*>(qrow + 16 * kk + 8 * kg);
   }
-
   // ---- staging
   // Piece i of thread t is key lkey + KSTEP i, 16-byte slot lc of that LDS
   // row. All of a wave's lanes fall in one page for a given i, so each load
@@ -530,7 +599,6 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   // The last K copies issued may still be in flight (into a slot nothing
   // reads any more); let them land before the workgroup's LDS is released.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
   // The output row's head and bound again, from a copy of the lane index
   // the compiler cannot see through: keeping the prologue's values alive
   // across the walk would cost registers the walk needs.
@@ -541,6 +609,96 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
   const int r_e = 32 * wave + col_e;
   const bool row_ok = m0 + r_e / GS < q_len;
   const int head_e = kvh * a.G + gsub * GS + r_e % GS;
+
+  if constexpr (SK) {
+    // A stream-K piece. Its (O, m, l) live in a slot of the workspace per
+    // (share, kv-head group, wave), one f32x4 per (row block, quad) and lane
+    // and an (m, lsum) pair per lane: the lane layout of the registers, so
+    // that the workgroup finishing the unit reads back exactly its own lanes.
+    // The slot is written and read with agent-scope (sc1) accesses, which
+    // bypass the non-coherent L2 of the writer's and reader's XCDs; the
+    // writer's flag for (slot, wave) goes out once its stores are complete.
+    constexpr int SLOT_FLOATS = (ND * 16 + 2) * 64;  // per wave
+    constexpr int kSc1 = 16;                         // cache-policy bit: agent scope
+    auto slot_rsrc = [&](int s) {
+      float* base = a.sk_part + (static_cast<int64_t>(s) * Shape::kWaves + wave) * SLOT_FLOATS;
+      return __builtin_amdgcn_make_buffer_rsrc(base, 0, SLOT_FLOATS * 4, kBufferFlags);
+    };
+    if (slot >= 0) {
+      if (slot >= a.sk_shares) continue;  // (a plan outside its workspace: nothing is written)
+      const int s = slot * a.kvg + kvg_id;
+      const auto rs = slot_rsrc(s);
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4 v = f32x4{acc[nd][4 * q4], acc[nd][4 * q4 + 1], acc[nd][4 * q4 + 2], acc[nd][4 * q4 + 3]};
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, ((nd * 4 + q4) * 64 + lane_e) * 16,
+                                                 0, kSc1);
+        }
+      }
+      __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_run), __float_as_uint(lsum)}, rs,
+                                            (ND * 16 * 64 + 2 * lane_e) * 4, 0, kSc1);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      if (lane_e == 0) __hip_atomic_store(a.sk_flag + s * Shape::kWaves + wave, 1, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+      continue;
+    }
+    // The unit's last piece: fold in the pieces of the lower-numbered shares
+    // [fix_lo, fix_hi) (each wave its own rows), then write the output.
+    // (only shares below this one: whatever the plan holds, a wait is on a
+    // workgroup dispatched earlier)
+    const int c_end = min(fix_hi, r_unit);
+    for (int c = max(fix_lo, 0); c < c_end; ++c) {
+      const int s = c * a.kvg + kvg_id;
+      int32_t* flag = a.sk_flag + s * Shape::kWaves + wave;
+      for (int polls = 0;; ++polls) {
+        const int f = __builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        if (f != 0) break;
+        if (polls >= kSkMaxPolls) {
+          if (lane_e == 0) __hip_atomic_store(a.sk_err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      asm volatile("" ::: "memory");
+      const auto rs = slot_rsrc(s);
+      const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(rs, (ND * 16 * 64 + 2 * lane_e) * 4, 0, kSc1);
+      f32x4 po[ND * 4];
+#pragma unroll
+      for (int i = 0; i < ND * 4; ++i)
+        po[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (i * 64 + lane_e) * 16, 0, kSc1));
+      if (lane_e == 0) __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
+      const float m_c = __uint_as_float(ml[0]);
+      const float m_new = fmaxf(m_run, m_c);
+      const float a_own = fast_exp2(m_run - m_new), a_c = fast_exp2(m_c - m_new);
+      m_run = m_new;
+      lsum = lsum * a_own + __uint_as_float(ml[1]) * a_c;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[nd][i] = acc[nd][i] * a_own + po[nd * 4 + i / 4][i % 4] * a_c;
+      }
+    }
+    if (row_ok) {
+      const float inv = 1.f / (lsum + __shfl_xor(lsum, 32, 64));
+      const int pos = r_e / GS;
+      uint16_t* orow =
+          a.out + static_cast<int64_t>(qs + m0 + pos) * a.o_st + static_cast<int64_t>(head_e) * a.o_sh;
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x16& o = acc[nd];
+          const u32x2 w =
+              u32x2{pack2(Elem<DT>::from_f32(o[4 * q4] * inv), Elem<DT>::from_f32(o[4 * q4 + 1] * inv)),
+                    pack2(Elem<DT>::from_f32(o[4 * q4 + 2] * inv), Elem<DT>::from_f32(o[4 * q4 + 3] * inv))};
+          *reinterpret_cast<u32x2*>(orow + 32 * nd + 8 * q4 + 4 * kg_e) = w;
+        }
+      }
+    }
+    continue;
+  } else {
   const float l_row = lsum + __shfl_xor(lsum, 32, 64);  // both halves of the row's keys
 
   if (slot >= 0) {
@@ -581,7 +739,10 @@ __device__ __forceinline__ void prefill_unit(const PrefillArgs& a) {
       *reinterpret_cast<u32x2*>(orow + 32 * nd + 8 * q4 + 4 * kg_e) = w;
     }
   }
+  }
+  }  // pieces
 }
+
 
 template <int DT, int D>
 __global__ __launch_bounds__(256) void paged_prefill_merge_kernel(PrefillArgs a, const int32_t* merges,
@@ -631,16 +792,16 @@ __global__ __launch_bounds__(256) void paged_prefill_merge_kernel(PrefillArgs a,
 }
 
 // One kernel per register budget (the occupancy attribute takes a constant).
-template <int DT, int D, int GS>
+template <int DT, int D, int GS, bool SK>
 __global__ __launch_bounds__(PrefillShape<GS>::kThreads) __attribute__((amdgpu_waves_per_eu(2))) void
-paged_prefill_kernel(PrefillArgs a) {
-  prefill_unit<DT, D, GS>(a);
+paged_prefill_kernel(PrefillArgs) {
+  prefill_unit<DT, D, GS, SK>();
 }
 
-template <int DT, int D, int GS>
+template <int DT, int D, int GS, bool SK>
 __global__ __launch_bounds__(PrefillShape<GS>::kThreads) __attribute__((amdgpu_waves_per_eu(1))) void
-paged_prefill_kernel_1w(PrefillArgs a) {
-  prefill_unit<DT, D, GS>(a);
+paged_prefill_kernel_1w(PrefillArgs) {
+  prefill_unit<DT, D, GS, SK>();
 }
 
 template <int DT, int D>
@@ -652,17 +813,20 @@ static int launch_merge(const PrefillArgs& a, const int32_t* merges, int32_t num
   return static_cast<int>(hipGetLastError());
 }
 
+// num_programs: tile-table entries (or pieces); stream-K: shares per kv-head
+// group (a.sk_start set).
 template <int DT, int D, int GS>
 static int launch_prefill(const PrefillArgs& a, int num_programs, hipStream_t stream) {
   using Shape = PrefillShape<GS>;
-  const int64_t units = static_cast<int64_t>(num_programs) * Shape::kSub * a.kvg;
+  const int64_t units = static_cast<int64_t>(num_programs) * (a.sk_start ? 1 : Shape::kSub) * a.kvg;
   if (units > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>(units)), block(Shape::kThreads);
   if constexpr (PrefillOccupancy<D, GS>::kWavesPerEU == 1) {
-    hipLaunchKernelGGL((paged_prefill_kernel_1w<DT, D, GS>), dim3(static_cast<unsigned>(units)),
-                       dim3(Shape::kThreads), 0, stream, a);
+    if (a.sk_start) hipLaunchKernelGGL((paged_prefill_kernel_1w<DT, D, GS, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((paged_prefill_kernel_1w<DT, D, GS, false>), grid, block, 0, stream, a);
   } else {
-    hipLaunchKernelGGL((paged_prefill_kernel<DT, D, GS>), dim3(static_cast<unsigned>(units)), dim3(Shape::kThreads),
-                       0, stream, a);
+    if (a.sk_start) hipLaunchKernelGGL((paged_prefill_kernel<DT, D, GS, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((paged_prefill_kernel<DT, D, GS, false>), grid, block, 0, stream, a);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -693,7 +857,8 @@ static int prefill_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
                         const int32_t* merges, int32_t num_merges, int32_t num_slots, void* workspace,
                         int64_t workspace_bytes, void* out, int64_t out_stride_t, int64_t out_stride_h,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
-                        int32_t dtype, void* stream) {
+                        int32_t dtype, void* stream, const int32_t* sk_start = nullptr,
+                        const int32_t* sk_piece = nullptr) {
   if (num_units < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return NIMBUS_ERR_INVALID;
   if (block_size != 16) return NIMBUS_ERR_UNSUPPORTED;
@@ -704,7 +869,8 @@ static int prefill_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
   const int gs = G % 8 == 0 ? 8 : (G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1));
   if (num_units == 0) return NIMBUS_OK;
   if (!q || !k_cache || !v_cache || !block_tables || !query_start || !context_lens || !out) return NIMBUS_ERR_INVALID;
-  if (!pieces && (!prog_seq || !prog_m)) return NIMBUS_ERR_INVALID;
+  if (!pieces && !sk_start && (!prog_seq || !prog_m)) return NIMBUS_ERR_INVALID;
+  if (sk_start && !sk_piece) return NIMBUS_ERR_INVALID;
   if (num_blocks <= 0 || num_blocks > INT32_MAX || bt_width <= 0) return NIMBUS_ERR_INVALID;
   // Pages are read through buffer resources with 32-bit offsets: 16 token
   // rows of a page must span less than 2 GiB.
@@ -753,6 +919,31 @@ static int prefill_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
   a.gsplit = G / gs;
   a.kvg = num_kv_heads * a.gsplit;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.sk_start = sk_start;
+  a.sk_piece = sk_piece;
+  a.sk_part = nullptr;
+  a.sk_flag = nullptr;
+  a.sk_err = nullptr;
+  a.sk_shares = 0;
+  if (sk_start) {
+    // num_units counts the shares per kv-head group; every workgroup of the
+    // grid must be resident at once (two per CU).
+    int64_t cus = 0;
+    const int e = device_cus(&cus);
+    if (e != 0) return e;
+    if (static_cast<int64_t>(num_units) * a.kvg > 2 * cus) return NIMBUS_ERR_UNSUPPORTED;
+    const int waves = gs == 1 ? 2 : 4;
+    const int64_t slots = static_cast<int64_t>(num_units) * a.kvg * waves;
+    const int64_t flag_bytes = (slots * 4 + 255) / 256 * 256;
+    const int64_t need = flag_bytes + 256 + slots * (head_dim / 32 * 16 + 2) * 64 * 4;
+    if (workspace == nullptr || workspace_bytes < need) return NIMBUS_ERR_WORKSPACE;
+    if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return NIMBUS_ERR_ALIGNMENT;
+    char* ws = static_cast<char*>(workspace);
+    a.sk_flag = reinterpret_cast<int32_t*>(ws);
+    a.sk_err = reinterpret_cast<int32_t*>(ws + flag_bytes);
+    a.sk_part = reinterpret_cast<float*>(ws + flag_bytes + 256);
+    a.sk_shares = num_units;
+  }
 
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc;
@@ -810,4 +1001,44 @@ extern "C" int nimbus_paged_prefill_pieces(const void* q, int64_t q_stride_t, in
                       context_lens, nullptr, nullptr, pieces, num_pieces, merges, num_merges, num_slots, workspace,
                       workspace_bytes, out, out_stride_t, out_stride_h, num_heads, num_kv_heads, head_dim,
                       block_size, scale, dtype, stream);
+}
+
+// Stream-K workspace: the flags (zero before the first call; every call that
+// completes leaves them zero), an error word, then the split pieces' slots.
+static int64_t stream_slots(int32_t shares, int32_t num_heads, int32_t num_kv_heads) {
+  const int G = num_heads / num_kv_heads;
+  const int gs = G % 8 == 0 ? 8 : (G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1));
+  return static_cast<int64_t>(shares) * num_kv_heads * (G / gs) * (gs == 1 ? 2 : 4);
+}
+
+extern "C" int64_t nimbus_paged_prefill_stream_flag_bytes(int32_t num_shares, int32_t num_heads,
+                                                          int32_t num_kv_heads) {
+  if (num_shares < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return -1;
+  return (stream_slots(num_shares, num_heads, num_kv_heads) * 4 + 255) / 256 * 256 + 256;
+}
+
+extern "C" int64_t nimbus_paged_prefill_stream_workspace_bytes(int32_t num_shares, int32_t num_heads,
+                                                               int32_t num_kv_heads, int32_t head_dim) {
+  const int64_t flags = nimbus_paged_prefill_stream_flag_bytes(num_shares, num_heads, num_kv_heads);
+  if (flags < 0 || head_dim <= 0) return -1;
+  return flags + stream_slots(num_shares, num_heads, num_kv_heads) * (head_dim / 32 * 16 + 2) * 64 * 4;
+}
+
+extern "C" int nimbus_paged_prefill_stream(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                           const void* k_cache, const void* v_cache, int64_t num_blocks,
+                                           int64_t cache_stride_block, int64_t cache_stride_token,
+                                           int64_t cache_stride_head, const int32_t* block_tables, int64_t bt_stride,
+                                           int32_t bt_width, const int32_t* query_start,
+                                           const int32_t* context_lens, const int32_t* share_start,
+                                           const int32_t* pieces, int32_t num_shares, void* workspace,
+                                           int64_t workspace_bytes, void* out, int64_t out_stride_t,
+                                           int64_t out_stride_h, int32_t num_heads, int32_t num_kv_heads,
+                                           int32_t head_dim, int32_t block_size, float scale, int32_t dtype,
+                                           void* stream) {
+  if (!share_start || !pieces) return NIMBUS_ERR_INVALID;
+  return prefill_impl(q, q_stride_t, q_stride_h, k_cache, v_cache, num_blocks, cache_stride_block,
+                      cache_stride_token, cache_stride_head, block_tables, bt_stride, bt_width, query_start,
+                      context_lens, nullptr, nullptr, nullptr, num_shares, nullptr, 0, 0, workspace, workspace_bytes,
+                      out, out_stride_t, out_stride_h, num_heads, num_kv_heads, head_dim, block_size, scale, dtype,
+                      stream, share_start, pieces);
 }

@@ -191,6 +191,143 @@ def plan_pieces(query_start_host: list[int], context_lens_host: list[int], num_h
     return PrefillPieces(t, mt, slot)
 
 
+@dataclass
+class PrefillStream:
+    """A stream-K plan (nimbus_paged_prefill_stream): the batch's (unit, key
+    block) work laid end to end per kv-head group and cut into `num_shares`
+    equal contiguous shares, one workgroup each, every workgroup resident at
+    once. share_start [num_shares + 1] and pieces [n, 8] int32 live on the
+    device; the plan holds for the head shape it was made for."""
+
+    share_start: torch.Tensor
+    pieces: torch.Tensor
+    num_shares: int
+    num_heads: int
+    num_kv_heads: int
+
+
+SK_FIELDS = 8  # int32 per piece record: seq, m0, kb0, kb1, slot, fix_lo, fix_hi, 0
+MIN_SHARE_BLOCKS = 2  # a share covers at least this many key blocks, unless units alone need more shares
+_CUS: dict[int, int] = {}
+
+
+def _resident_workgroups(device) -> int:
+    """Prefill workgroups the device holds at once: two per CU."""
+    dev = torch.device(device)
+    if dev.type != "cuda":
+        return RESIDENT_WORKGROUPS
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    if index not in _CUS:
+        _CUS[index] = torch.cuda.get_device_properties(index).multi_processor_count
+    return 2 * _CUS[index]
+
+
+def stream_units(query_start_host: list[int], context_lens_host: list[int], num_heads: int, num_kv_heads: int):
+    """The units of one kv-head group in stream order (sequence, then query
+    position): (sequence, first query, key blocks) arrays, and the number of
+    kv-head groups. A unit is POS = min(128 / GS, 64) query positions of GS
+    query heads (the kernel's 128 rows); its key blocks are the 64-key blocks
+    its last query sees."""
+    g = num_heads // num_kv_heads
+    gs = 8 if g % 8 == 0 else 4 if g % 4 == 0 else 2 if g % 2 == 0 else 1
+    pos = min(128 // gs, BLOCK_M)
+    qs = np.asarray(query_start_host, dtype=np.int64)
+    lens = np.diff(qs) if qs.size > 1 else np.zeros(0, dtype=np.int64)
+    ctx = np.asarray(context_lens_host, dtype=np.int64)
+    nu = (np.maximum(lens, 0) + pos - 1) // pos
+    useq = np.repeat(np.arange(lens.size, dtype=np.int64), nu)
+    um0 = (np.arange(useq.size) - np.repeat(np.cumsum(nu) - nu, nu)) * pos
+    kv_end = np.clip(np.minimum(ctx[useq], ctx[useq] - lens[useq] + um0 + pos), 0, None)
+    return useq, um0, (kv_end + KEY_BLOCK - 1) // KEY_BLOCK, num_kv_heads * (g // gs)
+
+
+def plan_stream(query_start_host: list[int], context_lens_host: list[int], num_heads: int, num_kv_heads: int,
+                device, resident: int | None = None) -> PrefillStream | None:
+    """Stream-K plan of a prefill batch; None when it has no queries.
+
+    Per kv-head group, the units' key blocks are laid end to end (a unit
+    with none counts one) and cut into S equal contiguous shares, S = the
+    workgroups the chip holds at once per group, fewer for a short batch
+    (shares of at least MIN_SHARE_BLOCKS blocks, but at least one share per
+    unit). Workgroup (share j, group g) is grid index j * groups + g, so a
+    group keeps its XCDs and their L2 as in the tile grid. A unit inside one
+    share is written whole. A unit cut by share boundaries is finished by the
+    share holding its last blocks (the fixer), which folds in the (O, m, l)
+    pieces the lower shares wrote (contributors); every wait is therefore on
+    a lower-numbered workgroup, dispatched earlier. Each share runs its
+    pieces last-first: its contributor piece (the head of the unit it shares
+    with the next share) first, so that piece is ready long before its fixer
+    asks for it, and its fixer piece last."""
+    useq, um0, nb, kvg = stream_units(query_start_host, context_lens_host, num_heads, num_kv_heads)
+    n = useq.size
+    if n == 0:
+        return None
+    cost = np.maximum(nb, 1)
+    total = int(cost.sum())
+    held = (resident or _resident_workgroups(device)) // kvg
+    if held < 1:
+        raise ValueError("the device holds fewer workgroups than one per kv-head group")
+    shares = max(1, min(held, max(n, -(-total // MIN_SHARE_BLOCKS))))
+    bounds = (np.arange(shares + 1, dtype=np.int64) * total) // shares
+    ustart = np.cumsum(cost) - cost
+    j0 = np.searchsorted(bounds, ustart, side="right") - 1
+    j1 = np.searchsorted(bounds, ustart + cost - 1, side="right") - 1
+    npc = j1 - j0 + 1
+    pu = np.repeat(np.arange(n), npc)                              # unit of each piece
+    pj = np.repeat(j0, npc) + (np.arange(pu.size) - np.repeat(np.cumsum(npc) - npc, npc))  # its share
+    kb0 = np.maximum(bounds[pj], ustart[pu]) - ustart[pu]
+    kb1 = np.minimum(bounds[pj + 1], ustart[pu] + cost[pu]) - ustart[pu]
+    first, last = pj == j0[pu], pj == j1[pu]
+    kb0[first] = 0
+    kb1[last] = 2**31 - 1
+    split = npc[pu] > 1
+    slot = np.where(split & ~last, pj, -1)
+    fix_lo = np.where(split & last, j0[pu], 0)
+    fix_hi = np.where(split & last, j1[pu], 0)
+    order = np.lexsort((-pu, pj))  # by share, then last piece first
+    rec = np.zeros((pu.size, SK_FIELDS), dtype=np.int32)
+    for col, arr in enumerate((useq[pu], um0[pu], kb0, kb1, slot, fix_lo, fix_hi)):
+        rec[:, col] = arr[order]
+    start = np.zeros(shares + 1, dtype=np.int32)
+    start[1:] = np.cumsum(np.bincount(pj, minlength=shares))
+    return PrefillStream(_to_device(start, device), _to_device(rec, device), shares, num_heads, num_kv_heads)
+
+
+def stream_workspace_bytes(num_shares: int, heads: int, kv_heads: int, head_dim: int) -> int:
+    """Workspace bytes of a PrefillStream plan of num_shares shares."""
+    return int(_lib.load().nimbus_paged_prefill_stream_workspace_bytes(num_shares, heads, kv_heads, head_dim))
+
+
+# Stream-K workspaces per (device, stream), zeroed when allocated: the plan's
+# flags must start at zero, and every call that completes leaves them zero.
+# Outgrown ones stay alive (a captured graph may still use them).
+_STREAM_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+_STREAM_OUTGROWN: list[torch.Tensor] = []
+
+
+def new_stream_workspace(nbytes: int, device) -> torch.Tensor:
+    """A zeroed workspace for nimbus_paged_prefill_stream calls of up to nbytes."""
+    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _stream_workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, torch._C._cuda_getCurrentRawStream(index))
+    ws = _STREAM_WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _STREAM_OUTGROWN.append(ws)
+        ws = _STREAM_WORKSPACES[key] = new_stream_workspace(max(nbytes, 8 << 20), device)
+    return ws
+
+
+def stream_error(workspace: torch.Tensor, num_shares: int, heads: int, kv_heads: int) -> int:
+    """The error word of a stream-K workspace (nonzero once a fix-up wait gave
+    up: the plan was inconsistent); reads the device."""
+    off = int(_lib.load().nimbus_paged_prefill_stream_flag_bytes(num_shares, heads, kv_heads)) - 256
+    return int(workspace[off:off + 4].view(torch.int32).item())
+
+
 def pieces_workspace_bytes(num_slots: int, heads: int, head_dim: int) -> int:
     """Workspace bytes of a PrefillPieces plan with num_slots split slots."""
     return int(_lib.load().nimbus_paged_prefill_pieces_workspace_bytes(num_slots, heads, head_dim))
@@ -275,6 +412,20 @@ def paged_prefill_attention(
               block_tables.stride(0), block_tables.shape[1], query_start.data_ptr(), context_lens.data_ptr())
     tail = (out.data_ptr(), out.stride(0), out.stride(1), h, kv, d, k_cache.shape[1], float(scale),
             _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    if isinstance(programs, PrefillStream):
+        if (programs.num_heads, programs.num_kv_heads) != (h, kv):
+            raise ValueError("the stream plan was made for another head shape")
+        need = lib.nimbus_paged_prefill_stream_workspace_bytes(programs.num_shares, h, kv, d)
+        if workspace is not None:
+            if workspace.nbytes < need or not workspace.is_cuda:
+                raise ValueError(f"workspace smaller than the {need} bytes this call needs")
+            ws = workspace
+        else:
+            ws = _stream_workspace(need, q.device)
+        rc = lib.nimbus_paged_prefill_stream(*common, programs.share_start.data_ptr(), programs.pieces.data_ptr(),
+                                             programs.num_shares, ws.data_ptr(), ws.nbytes, *tail)
+        _lib.check(rc, "nimbus_paged_prefill_stream")
+        return out
     if isinstance(programs, PrefillPieces):
         need = lib.nimbus_paged_prefill_pieces_workspace_bytes(programs.num_slots, h, d)
         if workspace is not None:

@@ -362,3 +362,75 @@ def test_verify_graph_loader_refuses_a_short_block_table():
     seqs = [workloads.SeqState(list(range(9)), [1]), workloads.SeqState(list(range(17)), [2])]
     with pytest.raises(IndexError, match="sequence 1"):
         g._load(seqs, 2)
+
+
+def _stream_case(lens, prefix):
+    qs = [0]
+    for n in lens:
+        qs.append(qs[-1] + n)
+    return qs, [p + n for p, n in zip(prefix, lens)]
+
+
+@pytest.mark.parametrize("lens,prefix,heads,kv", [
+    ([512] * 4, [831, 87, 183, 242], 32, 8),   # BASELINE config 4's prefill part (its seed's prefixes)
+    ([300, 17, 64, 0, 1, 900], [0, 5000, 64, 12, 0, 33], 32, 8),
+    ([8192], [0], 32, 8),                       # one long prompt: many units per share
+    ([130, 64, 40], [4000, 8000, 300], 32, 8),  # few heavy units: units cut across many shares
+    ([100, 250, 33], [10, 0, 700], 32, 4),      # TinyLlama heads (GS 8)
+    ([70, 9], [0, 3], 28, 4),                   # GQA 7: GS 1, 64-position units
+    ([1], [0], 32, 32),                         # MHA, a single query
+])
+def test_stream_plan_covers_every_block_once(lens, prefix, heads, kv):
+    """Every unit's key blocks are covered exactly once by its pieces; a cut
+    unit is finished by the share holding its last blocks, which folds in
+    exactly the lower shares that wrote its other pieces (each into its own
+    share's slot, at most one per share); each share runs its pieces
+    last-first; shares are balanced to a block and fit the resident
+    workgroups."""
+    from nimbus_amd.kernels.prefill_attention import plan_stream, stream_units
+
+    qs, ctx = _stream_case(lens, prefix)
+    resident = 512
+    plan = plan_stream(qs, ctx, heads, kv, "cpu", resident=resident)
+    useq, um0, nb, kvg = stream_units(qs, ctx, heads, kv)
+    assert plan.num_shares * kvg <= resident
+    start, rec = plan.share_start.numpy(), plan.pieces.numpy()
+    assert start[0] == 0 and start[-1] == len(rec) and np.all(np.diff(start) >= 0)
+    share_of = np.repeat(np.arange(plan.num_shares), np.diff(start))
+    unit_index = {(int(s), int(m)): i for i, (s, m) in enumerate(zip(useq, um0))}
+    pieces_of = {}
+    loads = np.zeros(plan.num_shares, dtype=np.int64)
+    for j, r in zip(share_of, rec):
+        u = unit_index[(int(r[0]), int(r[1]))]
+        hi = min(int(r[3]), int(nb[u]))
+        pieces_of.setdefault(u, []).append((int(r[2]), hi, int(r[4]), int(r[5]), int(r[6]), int(j)))
+        loads[j] += max(hi - int(r[2]), 0) + (1 if nb[u] == 0 else 0)
+    assert sorted(pieces_of) == list(range(len(useq)))
+    for u, ps in pieces_of.items():
+        ps.sort()
+        assert ps[0][0] == 0 and ps[-1][1] == nb[u]
+        assert all(a[1] == b[0] for a, b in zip(ps, ps[1:]))
+        finishers = [p for p in ps if p[2] == -1]
+        assert len(finishers) == 1
+        fin = finishers[0]
+        contributors = sorted(p[5] for p in ps if p[2] != -1)
+        assert all(p[2] == p[5] for p in ps if p[2] != -1)  # a contributor writes its own share's slot
+        if contributors:
+            assert fin[5] > contributors[-1] and (fin[3], fin[4]) == (contributors[0], fin[5])
+            assert contributors == list(range(contributors[0], fin[5]))
+        else:
+            assert (fin[3], fin[4]) == (0, 0)
+    for j in range(plan.num_shares):
+        rows = rec[start[j]:start[j + 1]]
+        assert sum(1 for r in rows if r[4] != -1) <= 1
+        order = [unit_index[(int(r[0]), int(r[1]))] for r in rows]
+        assert order == sorted(order, reverse=True)  # last piece first
+    total = int(np.maximum(nb, 1).sum())
+    assert loads.sum() == total and loads.max() - loads.min() <= 1
+
+
+def test_stream_plan_of_an_empty_batch_is_none():
+    from nimbus_amd.kernels.prefill_attention import plan_stream
+
+    assert plan_stream([0], [], 32, 8, "cpu") is None
+    assert plan_stream([0, 0, 0], [5, 9], 32, 8, "cpu") is None
