@@ -303,15 +303,7 @@ __device__ __forceinline__ void prefill_unit() {
   const int kbeg = min(kb0, n_kb_all);
   const int kend = min(kb1, n_kb_all);
 
-  int tid = threadIdx.x;
-  if constexpr (SK) {
-    // (formed again for each piece from the lane count and a wave index the
-    // compiler cannot see through, so that the lane-dependent offsets below
-    // are not kept live across all the pieces)
-    int w = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
-    asm volatile("" : "+s"(w));
-    tid = 64 * w + __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-  }
+  const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / 64) & (Shape::kWaves - 1);  // scalar, range known
   const int lane = tid % 64;
   const int col = lane % 32;  // this lane's row of the wave's 32

@@ -242,7 +242,7 @@ def stream_units(query_start_host: list[int], context_lens_host: list[int], num_
 
 
 def plan_stream(query_start_host: list[int], context_lens_host: list[int], num_heads: int, num_kv_heads: int,
-                device, resident: int | None = None) -> PrefillStream | None:
+                device, resident: int | None = None, min_share: int = MIN_SHARE_BLOCKS) -> PrefillStream | None:
     """Stream-K plan of a prefill batch; None when it has no queries.
 
     Per kv-head group, the units' key blocks are laid end to end (a unit
@@ -267,7 +267,7 @@ def plan_stream(query_start_host: list[int], context_lens_host: list[int], num_h
     held = (resident or _resident_workgroups(device)) // kvg
     if held < 1:
         raise ValueError("the device holds fewer workgroups than one per kv-head group")
-    shares = max(1, min(held, max(n, -(-total // MIN_SHARE_BLOCKS))))
+    shares = max(1, min(held, max(n, -(-total // min_share))))
     bounds = (np.arange(shares + 1, dtype=np.int64) * total) // shares
     ustart = np.cumsum(cost) - cost
     j0 = np.searchsorted(bounds, ustart, side="right") - 1
