@@ -328,6 +328,9 @@ def stream_error(workspace: torch.Tensor, num_shares: int, heads: int, kv_heads:
     return int(workspace[off:off + 4].view(torch.int32).item())
 
 
+_PIECES_WORKSPACES: dict = {}  # the pieces plans' workspaces, apart from the decode ones
+
+
 def pieces_workspace_bytes(num_slots: int, heads: int, head_dim: int) -> int:
     """Workspace bytes of a PrefillPieces plan with num_slots split slots."""
     return int(_lib.load().nimbus_paged_prefill_pieces_workspace_bytes(num_slots, heads, head_dim))
@@ -433,7 +436,7 @@ def paged_prefill_attention(
                 raise ValueError(f"workspace smaller than the {need} bytes this call needs")
             ws = workspace
         else:
-            ws = _cached_workspace(need, q.device)
+            ws = _cached_workspace(need, q.device, _PIECES_WORKSPACES)
         rc = lib.nimbus_paged_prefill_pieces(
             *common, programs.pieces.data_ptr(), programs.pieces.shape[0], programs.merges.data_ptr(),
             programs.merges.shape[0], programs.num_slots, ws.data_ptr(), ws.numel() * ws.element_size(), *tail)

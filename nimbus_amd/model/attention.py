@@ -81,23 +81,17 @@ class AttentionBackend:
         self._build_programs = prefill_attention.build_programs
 
     def _prefill_workspace(self, meta: AttnMetadata, q: torch.Tensor) -> torch.Tensor | None:
-        """This backend's workspace for a prefill call when it holds what the
-        call needs (the verify form's pieces, or a PrefillPieces plan's
-        slots), else None: the call then takes the per-stream cached
-        workspace. A workspace sized for decode alone (DecodeGraphs gives the
-        model's backend one) can be smaller than a key-range plan of an eager
-        chunked-prefill step needs."""
+        """This backend's workspace for a prefill call in the verify form
+        (the decode kernels) when it holds what the call needs, else None: the
+        call then takes the per-stream cached workspace. A PrefillPieces plan
+        never gets it: its slots start at the first byte, where a decode
+        workspace keeps the one-launch merge's counters."""
         ws = self.decode_workspace
-        if ws is None:
+        if ws is None or meta.prefill_kernel != "verify":
             return None
         h, d = q.shape[1], q.shape[2]
-        if meta.prefill_kernel == "verify":
-            need = paged_attention.verify_workspace_bytes(meta.num_prefills, meta.prefill_query_start_host[1], h, d,
-                                                          meta.prefill_block_tables.shape[1] * paged_attention.PAGE)
-        elif isinstance(meta.prefill_programs, prefill_attention.PrefillPieces):
-            need = prefill_attention.pieces_workspace_bytes(meta.prefill_programs.num_slots, h, d)
-        else:
-            return None  # the plain tile table needs no workspace
+        need = paged_attention.verify_workspace_bytes(meta.num_prefills, meta.prefill_query_start_host[1], h, d,
+                                                      meta.prefill_block_tables.shape[1] * paged_attention.PAGE)
         return ws if ws.numel() * ws.element_size() >= need else None
 
     def forward(
