@@ -19,6 +19,10 @@ import torch
 from nimbus_amd import _lib
 from nimbus_amd.kernels.paged_attention import _cached_workspace
 
+# The split-K partials' workspaces, apart from the decode ones (whose first
+# bytes are the decode merge's counters).
+_INT8_WORKSPACES: dict = {}
+
 
 def int8_matmul_workspace_bytes(m: int, n: int, k: int) -> int:
     return int(_lib.load().nimbus_int8_matmul_workspace_bytes(m, n, k))
@@ -68,7 +72,7 @@ def int8_matmul(x: torch.Tensor, w_q: torch.Tensor, scale: torch.Tensor, out: to
             raise ValueError(f"workspace smaller than the {need} bytes this call needs")
         ws = workspace
     else:
-        ws = _cached_workspace(need, x.device) if need > 0 else None
+        ws = _cached_workspace(need, x.device, _INT8_WORKSPACES) if need > 0 else None
     rc = lib.nimbus_int8_matmul(
         x2.data_ptr(), x2.stride(0), w_q.data_ptr(), w_q.stride(0), scale.data_ptr(), y.data_ptr(), y.stride(0),
         m, n, k, ws.data_ptr() if ws is not None else None,
@@ -223,7 +227,7 @@ def int8_matmul_packed(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Ten
             raise ValueError(f"workspace smaller than the {need} bytes this call needs")
         ws = workspace
     else:
-        ws = _cached_workspace(need, x.device) if need > 0 else None
+        ws = _cached_workspace(need, x.device, _INT8_WORKSPACES) if need > 0 else None
     ws_ptr = ws.data_ptr() if ws is not None else None
     ws_bytes = ws.numel() * ws.element_size() if ws is not None else 0
     if plan is None:

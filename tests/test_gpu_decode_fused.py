@@ -101,3 +101,38 @@ def test_one_workspace_across_shapes_and_a_graph():
         assert _clear(ws)
         paged_decode_attention(q20, k, v, ctx20, bt20, 8192, scale, workspace=ws)  # eager work between replays
     assert decode_workspace_error(ws) == 0
+
+
+def test_other_kernels_leave_the_cached_decode_workspace_alone():
+    """The INT8 matmul's split-K partials and the prefill pieces' slots write
+    their workspaces from the first byte: they keep caches of their own, so
+    the decode workspace cached per stream keeps zero counters and the next
+    decode and verify calls (taking it by default) stay right."""
+    announce("fused decode after INT8 split-K and prefill pieces")
+    from nimbus_amd.kernels import paged_attention as pa
+    from nimbus_amd.kernels.int8_matmul import int8_matmul, int8_matmul_workspace_bytes
+    from nimbus_amd.kernels.prefill_attention import paged_prefill_attention, plan_pieces
+    from nimbus_amd.quant import quantize_weight
+
+    g = torch.Generator(device="cuda").manual_seed(3)
+    used = 0
+    for m, n, kdim in ((64, 6144, 4096), (64, 4096, 14336), (16, 4096, 4096), (1, 28672, 4096)):
+        if int8_matmul_workspace_bytes(m, n, kdim) > 0:
+            used += 1
+            wq, sc = quantize_weight((torch.randn(n, kdim, generator=g, device="cuda") * 0.02).bfloat16())
+            int8_matmul(torch.randn(m, kdim, generator=g, device="cuda").bfloat16(), wq, sc)
+    assert used > 0
+    b = workloads.build_batch([(8192 + 64, 64)], heads=32, kv_heads=8, head_dim=128, dtype=torch.bfloat16,
+                              device="cuda", seed=4, write_first=False)
+    args = b.prefill_args()
+    plan = plan_pieces(args[7], args[8], 32, 8, "cuda")
+    assert plan is not None
+    paged_prefill_attention(*args, plan)
+    lens = workloads.llama3_decode_lens(seed=5, batch=64)
+    q, k, v, ctx, bt, scale = _case(32, 8, 128, lens, torch.bfloat16, seed=5)
+    got = paged_decode_attention(q, k, v, ctx, bt, max(lens), scale)  # the cached workspace
+    torch.cuda.synchronize()
+    ws = pa._WORKSPACES[(torch.cuda.current_device(), torch._C._cuda_getCurrentRawStream(torch.cuda.current_device()))]
+    assert _clear(ws) and decode_workspace_error(ws) == 0
+    own = new_decode_workspace(decode_workspace_bytes(64, 32, 128, max(lens)), "cuda")
+    assert torch.equal(got, _two_launch(q, k, v, ctx, bt, max(lens), scale, own))
