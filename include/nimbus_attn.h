@@ -71,16 +71,10 @@ int nimbus_write_kv(const void* k, const void* v, void* k_cache, void* v_cache, 
  * Bytes of workspace nimbus_paged_decode needs at this batch, head count,
  * head dim and max_context (a pure function of its arguments): the batch's
  * page prefix sum and room for fp32 (O, m, l) pieces of sequences whose
- * pages are split between waves, after NIMBUS_DECODE_COUNTER_BYTES of piece
- * counters and an error word at its start. Those first bytes must be zero
- * before the first call and must not be written by anything else; every
- * completed call leaves them zero (the error word turns nonzero only if a
- * merge ever stops waiting for its pieces), whatever the shape of the calls
- * that share the workspace. The rest needs no initialisation and carries
- * nothing between calls. Calls that run concurrently (on different streams)
- * need different workspaces.
+ * pages are split between waves. The workspace carries nothing from one call
+ * to the next and needs no initialisation; calls that run concurrently (on
+ * different streams) need different workspaces.
  */
-#define NIMBUS_DECODE_COUNTER_BYTES (8192 * 4 + 256)
 int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
                                             int64_t max_context);
 
@@ -94,10 +88,7 @@ int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, in
  * kv head h / (num_heads / num_kv_heads). q/out: element (b, h, d) at
  * b*stride_b + h*stride_h + d. The batch's 16-token pages are split evenly
  * over a fixed number of waves per kv-head group (a split may fall inside a
- * sequence; a second pass merges such sequences' pieces: in the same launch,
- * by workgroups dispatched after the page pass's, when the workgroups hold at
- * least 256 threads and batch x kv-head groups <= 8192; else a second
- * launch). The launch grid
+ * sequence; a second pass merges such sequences' pieces). The launch grid
  * depends only on batch, num_kv_heads, max_context (which must be >= every
  * context length; longer contexts are cut to it) and the device's CU count,
  * so a fixed max_context gives a graph-capturable call. batch <= 4096. Page

@@ -107,27 +107,7 @@ struct DecodeArgs {
   int32_t wgc;       // workgroups per slice: kvg / wgw
   int32_t max_ctx;   // context bound: min(max_context, block-table width * 16)
   float scale_log2;
-  // Fused merge (a one-launch call): workgroups past the page pass's page_wgs
-  // merge the split sequences, each (sequence, kv group) once the page waves
-  // have counted all its pieces in counters[b * kvg + kg] (zero before the
-  // call, reset to zero by the merge); err is set if a merge stops waiting.
-  int32_t fused;
-  int32_t page_wgs;
-  int32_t* counters;
-  int32_t* err;
 };
-
-// Decode workspace: its first kDecodeCounterBytes hold the fused merge's
-// piece counters and error word, at a fixed place whatever the call's shape
-// (so calls of different shapes can share a workspace); zero before the first
-// call, and every completed call leaves them zero.
-constexpr int kMaxFusedCounters = 8192;
-constexpr int64_t kDecodeCounterBytes = NIMBUS_DECODE_COUNTER_BYTES;
-static_assert(kDecodeCounterBytes == kMaxFusedCounters * 4 + 256, "counters, then the error word");
-constexpr int kSc1 = 16;  // buffer cache-policy bit: agent scope (through to memory, past the XCD's L2)
-// Polls of the fused merge's wait before it gives up and sets err (its
-// pieces come from page workgroups dispatched before it, so the wait ends).
-constexpr int kMergeMaxPolls = 1 << 22;
 
 __device__ __forceinline__ int clamp_page(int32_t pid, int32_t nb) {
   return static_cast<uint32_t>(pid) < static_cast<uint32_t>(nb) ? pid : 0;
@@ -236,211 +216,6 @@ __device__ __forceinline__ int v_pos(int r, int c) {
   return D == 128 ? c ^ ((2 * r) & 15) : c ^ (r & 6);
 }
 
-constexpr int kMergeBatch = 8;
-constexpr int kMergeThreads = 256;  // 16 columns x D / 8 lanes (D <= 128)
-constexpr int kMergeLdsBytes = kMergeThreads * (4 + 4 + 32);  // per merged (sequence, kv group): M, L, O
-
-// Merge of one (sequence, kv group) over its pieces [i0, i1], by one
-// kMergeThreads-thread group e (0..255) whose M, L, O meet in the LDS at sm,
-// sl, so (kMergeThreads each): the rule of paged_decode_merge_kernel below.
-// Returns the thread's combined row when it is the group's writer (grp 0).
-// SC1: read the pieces with agent-scope loads (written by another XCD's waves
-// during this launch).
-template <int D, bool SC1>
-__device__ __forceinline__ bool merge_pieces(const DecodeArgs& a, int b, int kg, int i0, int i1, int e, float* sm,
-                                             float* sl, f32x4* so, bool active, float& L_out, f32x4& O0_out,
-                                             f32x4& O1_out, int& qj_out, int& head_out, int& d0_out) {
-  constexpr int SEG = D / 8;  // lanes per column
-  const int kvh = kg % a.nkv;
-  const int g0 = (kg / a.nkv) * 16;
-  const int gcount = min(16, a.nq * a.G - g0);
-  const int lanes = gcount * SEG;            // lanes of one piece group
-  const int groups = kMergeThreads / lanes;  // >= 1
-  const int grp = e / lanes;
-  const int el = e - grp * lanes;
-  const int vcol = g0 + el / SEG;
-  const int qj = vcol / a.G;
-  const int head = kvh * a.G + vcol - qj * a.G;
-  const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;
-  const int64_t cols = static_cast<int64_t>(a.nq) * a.H;  // rows per slot
-  const int d0 = 8 * (el % SEG);
-
-  float M = kNoScore, L = 0.f;
-  f32x4 O0 = f32x4{0.f, 0.f, 0.f, 0.f}, O1 = O0;
-  if (active && grp < groups) {
-    for (int i = i0 + grp; i <= i1; i += groups * kMergeBatch) {
-      float2 ml[kMergeBatch];
-      f32x4 o0[kMergeBatch], o1[kMergeBatch];
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        const int64_t row = (static_cast<int64_t>(min(i + u * groups, i1)) + b) * cols + vhead;
-        if constexpr (SC1) {
-          const auto rm = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + row * 2, 0, 8, 0x00020000);
-          const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + row * D + d0, 0, 32, 0x00020000);
-          const u32x2 m2 = __builtin_amdgcn_raw_buffer_load_b64(rm, 0, 0, kSc1);
-          ml[u] = make_float2(__uint_as_float(m2[0]), __uint_as_float(m2[1]));
-          o0[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, 0, 0, kSc1));
-          o1[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ro, 16, 0, kSc1));
-        } else {
-          ml[u] = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
-          o0[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
-          o1[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
-        }
-      }
-      float mx = M;
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        if (i + u * groups <= i1) mx = fmaxf(mx, ml[u].x);
-      }
-      const float wo = fast_exp2(M - mx);
-      L *= wo;
-      O0 *= wo;
-      O1 *= wo;
-#pragma unroll
-      for (int u = 0; u < kMergeBatch; ++u) {
-        if (i + u * groups <= i1) {
-          const float wi = fast_exp2(ml[u].x - mx);
-          L += ml[u].y * wi;
-          O0 += o0[u] * wi;
-          O1 += o1[u] * wi;
-        }
-      }
-      M = mx;
-    }
-  }
-  // Groups without pieces keep M = kNoScore, L = 0, O = 0 and weigh nothing
-  // (group 0 always holds piece i0).
-  sm[e] = M;
-  sl[e] = L;
-  so[e] = O0;
-  so[kMergeThreads + e] = O1;
-  __syncthreads();
-  if (!active || grp != 0) return false;
-  for (int g = 1; g < groups; ++g) M = fmaxf(M, sm[g * lanes + el]);
-  const float w0 = fast_exp2(sm[el] - M);
-  L *= w0;
-  O0 *= w0;
-  O1 *= w0;
-  for (int g = 1; g < groups; ++g) {
-    const int j = g * lanes + el;
-    const float w = fast_exp2(sm[j] - M);
-    L += sl[j] * w;
-    O0 += so[j] * w;
-    O1 += so[kMergeThreads + j] * w;
-  }
-  L_out = L;
-  O0_out = O0;
-  O1_out = O1;
-  qj_out = qj;
-  head_out = head;
-  d0_out = d0;
-  return true;
-}
-
-template <int DT>
-__device__ __forceinline__ void write_merged(const DecodeArgs& a, int b, float L, f32x4 O0, f32x4 O1, int qj,
-                                             int head, int d0) {
-  const float inv = L > 0.f ? 1.f / L : 0.f;
-  const int64_t tok = static_cast<int64_t>(b) * a.nq + qj;
-  uint16_t* orow = a.out + tok * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
-  const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O0[0] * inv), Elem<DT>::from_f32(O0[1] * inv)),
-                        pack2(Elem<DT>::from_f32(O0[2] * inv), Elem<DT>::from_f32(O0[3] * inv)),
-                        pack2(Elem<DT>::from_f32(O1[0] * inv), Elem<DT>::from_f32(O1[1] * inv)),
-                        pack2(Elem<DT>::from_f32(O1[2] * inv), Elem<DT>::from_f32(O1[3] * inv))};
-  *reinterpret_cast<u32x4*>(orow) = w;
-}
-
-// (sequence, kv group) pairs one fused-merge workgroup of wgw waves takes:
-// kMergeThreads threads and kMergeLdsBytes of the V staging LDS each.
-template <int D>
-__host__ __device__ constexpr int fused_merge_pairs(int wgw) {
-  return (64 * wgw / kMergeThreads) < static_cast<int>(kMaxWgWaves * kPage * D * 2 / kMergeLdsBytes)
-             ? 64 * wgw / kMergeThreads
-             : static_cast<int>(kMaxWgWaves * kPage * D * 2 / kMergeLdsBytes);
-}
-
-// The fused merge: a workgroup past the page pass merges `pairs` (sequence,
-// kv group) pairs, kMergeThreads threads each (threads beyond them idle but
-// meet the barriers). A pair's pages and the batch's total come from the
-// context lengths (the page pass's prefix copy in the workspace may not be
-// written yet when this workgroup starts); its first thread wave waits until
-// the page waves have counted all its pieces, then resets the counter. The
-// workgroup is dispatched after every page workgroup, so it waits only on
-// work that has started.
-template <int DT, int D>
-__device__ void fused_merge(const DecodeArgs& a, unsigned char* lds, int pairs) {
-  __shared__ int red[kMaxWgWaves][2];
-  const int h = threadIdx.x / kMergeThreads;
-  const int e = threadIdx.x % kMergeThreads;
-  const int wave = threadIdx.x / 64;
-  const int lane = threadIdx.x % 64;
-  const int pair = (static_cast<int>(blockIdx.x) - a.page_wgs) * pairs + h;
-  const bool in = h < pairs && pair < a.B * a.kvg;
-  const int b = in ? pair / a.kvg : 0;
-  const int kg = in ? pair - b * a.kvg : 0;
-  // Pages before sequence b and in the whole batch.
-  int before = 0, all = 0;
-  for (int i = e; i < a.B; i += kMergeThreads) {
-    const int n = pages_of(a, i);
-    all += n;
-    if (i < b) before += n;
-  }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    before += __shfl_xor(before, off, 64);
-    all += __shfl_xor(all, off, 64);
-  }
-  if (lane == 0) {
-    red[wave][0] = before;
-    red[wave][1] = all;
-  }
-  __syncthreads();
-  const int w0 = (threadIdx.x / kMergeThreads) * (kMergeThreads / 64);
-  before = 0;
-  all = 0;
-  for (int w = w0; w < w0 + kMergeThreads / 64 && w < static_cast<int>(blockDim.x / 64); ++w) {
-    before += red[w][0];
-    all += red[w][1];
-  }
-  const int n_b = in ? pages_of(a, b) : 0;
-  bool split = in && all > 0 && n_b > 0;
-  int i0 = 0, i1 = 0;
-  if (split) {
-    const int nw = active_waves(all, a.nwk);
-    i0 = slice_owner(before, nw, all);
-    i1 = slice_owner(before + n_b - 1, nw, all);
-    split = i0 != i1;
-  }
-  if (split && e < 64) {
-    int* cnt = a.counters + b * a.kvg + kg;
-    const int want = i1 - i0 + 1;
-    for (int polls = 0;; ++polls) {
-      const int c = __builtin_amdgcn_readfirstlane(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      if (c >= want) break;
-      if (polls >= kMergeMaxPolls) {
-        if (lane == 0) __hip_atomic_store(a.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
-    }
-    if (lane == 0) __hip_atomic_store(cnt, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next call
-  }
-  __syncthreads();
-  const int hs = h < pairs ? h : 0;  // (idle threads write a slot nobody reads... of pair 0's region, unread by them)
-  float* base = reinterpret_cast<float*>(lds + hs * kMergeLdsBytes);
-  float L;
-  f32x4 O0, O1;
-  int qj, head, d0;
-  // (threads beyond the pairs take no part: they must only meet the barrier)
-  if (h < pairs) {
-    if (merge_pieces<D, true>(a, b, kg, i0, i1, e, base, base + kMergeThreads,
-                              reinterpret_cast<f32x4*>(base + 2 * kMergeThreads), split, L, O0, O1, qj, head, d0))
-      write_merged<DT>(a, b, L, O0, O1, qj, head, d0);
-  } else {
-    __syncthreads();
-  }
-}
-
 // STREAM: K/V pages are loaded nontemporally (streamed, not kept in the L2).
 // Every page is read once per launch when there is one column chunk, and
 // streaming measured 5-6% faster there (config 3's page pass 86.6-88.0 us
@@ -454,12 +229,6 @@ __device__ void fused_merge(const DecodeArgs& a, unsigned char* lds, int pairs) 
 template <int DT, int D, bool STREAM, bool REGP>
 __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_eu(2))) void paged_decode_kernel(
     DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t vbs[kMaxWgWaves][kPage * D];  // per wave: a page of V, swizzled
-  if (a.fused && static_cast<int>(blockIdx.x) >= a.page_wgs) {
-    // (a merge workgroup of a fused call: its LDS is the V staging area)
-    fused_merge<DT, D>(a, reinterpret_cast<unsigned char*>(&vbs[0][0]), fused_merge_pairs<D>(a.wgw));
-    return;
-  }
   // (takes the kernel arguments the first page loads need, so that their
   // loads go out with the first ones instead of after the prefix, a round
   // trip of their own)
@@ -471,6 +240,7 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
   constexpr int LPT = D / 8;              // lanes per token row (16 bytes each)
   constexpr int TPL = 64 / LPT;           // token rows per wave-wide load
   constexpr int VL = PageBuf<D>::VL;
+  __shared__ __attribute__((aligned(16))) uint16_t vbs[kMaxWgWaves][kPage * D];  // per wave: a page of V, swizzled
   extern __shared__ int pre[];  // [B + 1]
 
   const int wave = threadIdx.x / 64;
@@ -660,7 +430,6 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
   const int tr_chunk = (col % 4) / 2;
 
   int seg0 = lo;  // first flat page of the current piece
-  int pend0 = -1, pend1 = -1;  // counters of the pieces written (at most the slice's first and last sequence)
   float m_run = kNoScore;
   float l_run = 0.f;
   f32x4 acc[NN];
@@ -768,24 +537,12 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
             *reinterpret_cast<u32x2*>(orow + 16 * nn + 4 * grp) = w;
           }
         } else {
-          // (agent-scope stores: the fused merge may read them on another XCD)
           const int64_t row = (static_cast<int64_t>(idx) + rb) * a.nq * a.H + vhead;
-          const auto ro = __builtin_amdgcn_make_buffer_rsrc(a.part_o + row * D, 0, D * 4, 0x00020000);
+          float* po = a.part_o + row * D;
 #pragma unroll
-          for (int nn = 0; nn < NN; ++nn)
-            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[nn]), ro, (16 * nn + 4 * grp) * 4,
-                                                   0, kSc1);
-          if (grp == 0) {
-            const auto rm = __builtin_amdgcn_make_buffer_rsrc(a.part_ml + row * 2, 0, 8, 0x00020000);
-            __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(m_run), __float_as_uint(l)}, rm, 0, 0, kSc1);
-          }
+          for (int nn = 0; nn < NN; ++nn) *reinterpret_cast<f32x4*>(po + 16 * nn + 4 * grp) = acc[nn];
+          if (grp == 0) *reinterpret_cast<float2*>(a.part_ml + row * 2) = make_float2(m_run, l);
         }
-      }
-      if (!whole) {
-        // Counted for the fused merge once the walk is over (a wait for the
-        // stores here would drain the K/V loads in flight).
-        if (pend0 < 0) pend0 = rb * a.kvg + kg;
-        else pend1 = rb * a.kvg + kg;
       }
       m_run = kNoScore;
       l_run = 0.f;
@@ -808,13 +565,6 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
       step(buf[k], x + k);
     }
   }
-  if (a.fused && pend0 >= 0) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the pieces' stores are complete
-    if (lane == 0) {
-      __hip_atomic_fetch_add(a.counters + pend0, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (pend1 >= 0) __hip_atomic_fetch_add(a.counters + pend1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
 }
 
 // Second pass: for every sequence whose pages were split between waves,
@@ -828,11 +578,15 @@ __global__ __launch_bounds__(64 * kMaxWgWaves) __attribute__((amdgpu_waves_per_e
 // trip, every load of a batch issued before any is used. So a sequence's
 // pieces (tens for a long context) arrive in one or two round trips; the
 // groups' running (M, L, O) are then combined through LDS by the same rule.
+constexpr int kMergeBatch = 8;
+constexpr int kMergeThreads = 256;  // 16 columns x D / 8 lanes (D <= 128)
 
 template <int DT, int D>
 __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(DecodeArgs a) {
+  constexpr int SEG = D / 8;  // lanes per column
+  static_assert(16 * SEG <= kMergeThreads, "one lane per (column, 8 elements of d)");
   __shared__ float sm[kMergeThreads], sl[kMergeThreads];
-  __shared__ f32x4 so[2 * kMergeThreads];
+  __shared__ f32x4 so[2][kMergeThreads];
   const int b = blockIdx.x;
   const int kg = blockIdx.y;
   const int total = a.pre_out[a.B];
@@ -843,11 +597,83 @@ __global__ __launch_bounds__(kMergeThreads) void paged_decode_merge_kernel(Decod
   const int i0 = slice_owner(first, nw, total);
   const int i1 = slice_owner(last, nw, total);
   if (i0 == i1) return;
-  float L;
-  f32x4 O0, O1;
-  int qj, head, d0;
-  if (merge_pieces<D, false>(a, b, kg, i0, i1, threadIdx.x, sm, sl, so, true, L, O0, O1, qj, head, d0))
-    write_merged<DT>(a, b, L, O0, O1, qj, head, d0);
+  const int kvh = kg % a.nkv;
+  const int g0 = (kg / a.nkv) * 16;
+  const int gcount = min(16, a.nq * a.G - g0);
+  const int lanes = gcount * SEG;            // lanes of one piece group
+  const int groups = kMergeThreads / lanes;  // >= 1
+  const int e = threadIdx.x;
+  const int grp = e / lanes;
+  const int el = e - grp * lanes;
+  const int vcol = g0 + el / SEG;
+  const int qj = vcol / a.G;
+  const int head = kvh * a.G + vcol - qj * a.G;
+  const int64_t vhead = static_cast<int64_t>(qj) * a.H + head;
+  const int64_t cols = static_cast<int64_t>(a.nq) * a.H;  // rows per slot
+  const int d0 = 8 * (el % SEG);
+
+  float M = kNoScore, L = 0.f;
+  f32x4 O0 = f32x4{0.f, 0.f, 0.f, 0.f}, O1 = O0;
+  if (grp < groups) {
+    for (int i = i0 + grp; i <= i1; i += groups * kMergeBatch) {
+      float2 ml[kMergeBatch];
+      f32x4 o0[kMergeBatch], o1[kMergeBatch];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int64_t row = (static_cast<int64_t>(min(i + u * groups, i1)) + b) * cols + vhead;
+        ml[u] = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+        o0[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0);
+        o1[u] = *reinterpret_cast<const f32x4*>(a.part_o + row * D + d0 + 4);
+      }
+      float mx = M;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        if (i + u * groups <= i1) mx = fmaxf(mx, ml[u].x);
+      }
+      const float wo = fast_exp2(M - mx);
+      L *= wo;
+      O0 *= wo;
+      O1 *= wo;
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        if (i + u * groups <= i1) {
+          const float wi = fast_exp2(ml[u].x - mx);
+          L += ml[u].y * wi;
+          O0 += o0[u] * wi;
+          O1 += o1[u] * wi;
+        }
+      }
+      M = mx;
+    }
+  }
+  // Groups without pieces keep M = kNoScore, L = 0, O = 0 and weigh nothing
+  // (group 0 always holds piece i0).
+  sm[e] = M;
+  sl[e] = L;
+  so[0][e] = O0;
+  so[1][e] = O1;
+  __syncthreads();
+  if (grp != 0) return;
+  for (int g = 1; g < groups; ++g) M = fmaxf(M, sm[g * lanes + el]);
+  const float w0 = fast_exp2(sm[el] - M);
+  L *= w0;
+  O0 *= w0;
+  O1 *= w0;
+  for (int g = 1; g < groups; ++g) {
+    const int j = g * lanes + el;
+    const float w = fast_exp2(sm[j] - M);
+    L += sl[j] * w;
+    O0 += so[0][j] * w;
+    O1 += so[1][j] * w;
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  const int64_t tok = static_cast<int64_t>(b) * a.nq + qj;
+  uint16_t* orow = a.out + tok * a.o_sb + static_cast<int64_t>(head) * a.o_sh + d0;
+  const u32x4 w = u32x4{pack2(Elem<DT>::from_f32(O0[0] * inv), Elem<DT>::from_f32(O0[1] * inv)),
+                        pack2(Elem<DT>::from_f32(O0[2] * inv), Elem<DT>::from_f32(O0[3] * inv)),
+                        pack2(Elem<DT>::from_f32(O1[0] * inv), Elem<DT>::from_f32(O1[1] * inv)),
+                        pack2(Elem<DT>::from_f32(O1[2] * inv), Elem<DT>::from_f32(O1[3] * inv))};
+  *reinterpret_cast<u32x4*>(orow) = w;
 }
 
 // Waves the launch gives each kv-head group: what the chip keeps resident,
@@ -879,18 +705,12 @@ int device_cus(int64_t* cus) {
   return 0;
 }
 
-// phase bit 1: page pass, bit 2: merge pass. a.fused: both in one launch,
-// the merge workgroups appended to the page pass's grid.
+// phase bit 1: page pass, bit 2: merge pass.
 template <int DT, int D>
 static int launch_decode(const DecodeArgs& a, int phases, hipStream_t stream) {
   if (phases & 1) {
     const size_t dyn = static_cast<size_t>(a.B + 1) * sizeof(int);
-    int merge_wgs = 0;
-    if (a.fused) {
-      const int pairs = fused_merge_pairs<D>(a.wgw);
-      merge_wgs = (a.B * a.kvg + pairs - 1) / pairs;
-    }
-    const dim3 grid(a.nwk * a.wgc + merge_wgs), block(64 * a.wgw);
+    const dim3 grid(a.nwk * a.wgc), block(64 * a.wgw);
     const bool regp = a.B <= kRegPrefixBatch;
     if (a.gchunks == 1) {
       if (regp) hipLaunchKernelGGL((paged_decode_kernel<DT, D, true, true>), grid, block, dyn, stream, a);
@@ -900,7 +720,7 @@ static int launch_decode(const DecodeArgs& a, int phases, hipStream_t stream) {
       else hipLaunchKernelGGL((paged_decode_kernel<DT, D, false, false>), grid, block, dyn, stream, a);
     }
   }
-  if ((phases & 2) && !a.fused) {
+  if (phases & 2) {
     hipLaunchKernelGGL((paged_decode_merge_kernel<DT, D>), dim3(a.B, a.kvg), dim3(kMergeThreads), 0, stream, a);
   }
   return static_cast<int>(hipGetLastError());
@@ -926,7 +746,7 @@ static int64_t workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim
   // Any device and any kvg >= 1 launch at most this many waves per kv group.
   const int64_t slots = waves_per_group(kMaxResidentWaves, 1, max_pages_of(batch, max_context)) + batch;
   const int64_t cols = static_cast<int64_t>(num_heads) * nq;
-  return kDecodeCounterBytes + prefix_bytes(batch) + round256(slots * cols * 2 * 4) + slots * cols * head_dim * 4;
+  return prefix_bytes(batch) + round256(slots * cols * 2 * 4) + slots * cols * head_dim * 4;
 }
 
 extern "C" int64_t nimbus_paged_decode_workspace_bytes(int32_t batch, int32_t num_heads, int32_t head_dim,
@@ -1019,14 +839,6 @@ static int paged_decode_impl(int phases, int32_t nq, const void* q, int64_t q_st
   if (nwk * a.kvg > INT32_MAX / 2 || max_pages_of(batch, ctx_bound) > INT32_MAX / 2) return NIMBUS_ERR_UNSUPPORTED;
   const int64_t slots = nwk + batch;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  a.counters = reinterpret_cast<int32_t*>(ws);
-  a.err = reinterpret_cast<int32_t*>(ws + kMaxFusedCounters * 4);
-  a.page_wgs = static_cast<int32_t>(nwk * a.wgc);
-  // One launch when the merge workgroups fit the page pass's shape (at least
-  // kMergeThreads threads per workgroup) and the counters their place.
-  a.fused = phases == 3 && fused_merge_pairs<128>(a.wgw) >= 1 && (head_dim == 128 || fused_merge_pairs<64>(a.wgw) >= 1) &&
-            static_cast<int64_t>(batch) * a.kvg <= kMaxFusedCounters;
-  ws += kDecodeCounterBytes;
   a.pre_out = reinterpret_cast<int32_t*>(ws);
   a.part_ml = reinterpret_cast<float*>(ws + prefix_bytes(batch));
   const int64_t cols = static_cast<int64_t>(num_heads) * nq;
@@ -1072,12 +884,9 @@ extern "C" int nimbus_paged_decode_merge(NIMBUS_DECODE_PARAMS) {
 // names a host-side stand-in, not device memory: the device address comes
 // from hipGetSymbolAddress, asked once per device (with that device
 // current) on the entry point's first call there, and only that address is
-// handed to kernels. The workspace's piece counters (its first
-// kDecodeCounterBytes) must start at zero: a device array starts zeroed,
-// and every completed call leaves them zero; the rest needs no
-// initialisation (the page pass writes the prefix sum and every piece before
-// the merge reads them), so nothing is cleared. Calls that overlap on one
-// device race on it.
+// handed to kernels. The decode workspace needs no initialisation (the page
+// pass writes the prefix sum and every piece before the merge reads them),
+// so nothing is cleared. Calls that overlap on one device race on it.
 constexpr int64_t kNoAllocScratchBytes = NIMBUS_NOALLOC_SCRATCH_BYTES;
 static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 

@@ -19,8 +19,7 @@ import torch
 from nimbus_amd import _lib
 from nimbus_amd.kernels.paged_attention import _cached_workspace
 
-# The split-K partials' workspaces, apart from the decode ones (whose first
-# bytes are the decode merge's counters).
+# The split-K partials' workspaces (a family apart from the decode ones).
 _INT8_WORKSPACES: dict = {}
 
 

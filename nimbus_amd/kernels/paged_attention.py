@@ -47,29 +47,15 @@ _WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
 _OUTGROWN: list[torch.Tensor] = []
 
 
-# The decode workspace's first COUNTER_BYTES hold the one-launch merge's
-# piece counters and an error word (NIMBUS_DECODE_COUNTER_BYTES): zero before
-# the first call, left zero by every completed call, written by nothing else.
-COUNTER_BYTES = 8192 * 4 + 256
-
-
 def new_decode_workspace(nbytes: int, device) -> torch.Tensor:
-    """A zeroed workspace of at least nbytes for decode and verify calls
-    (its counter region must start at zero; the rest needs no initialisation)."""
-    return torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
-
-
-def decode_workspace_error(workspace: torch.Tensor) -> int:
-    """The decode workspace's error word: nonzero once a one-launch merge
-    stopped waiting for its pieces (it never should); reads the device."""
-    return int(workspace[COUNTER_BYTES - 256:COUNTER_BYTES - 252].view(torch.int32).item())
+    """A workspace of at least nbytes for decode calls (no initialisation needed)."""
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
 def _cached_workspace(nbytes: int, device: torch.device, cache: dict | None = None) -> torch.Tensor:
-    """A decode workspace per (device, stream), grown on demand; `cache`
-    keeps another family of workspaces (the prefill pieces' plans, whose
-    slots start at the first byte and must not share a decode workspace's
-    counters)."""
+    """A workspace per (device, stream), grown on demand; `cache` keeps
+    another family of them (the prefill pieces' and the INT8 matmul's), so a
+    call of one family never grows or reuses another's buffer."""
     cache = _WORKSPACES if cache is None else cache
     index = device.index if device.index is not None else torch.cuda.current_device()
     key = (index, torch._C._cuda_getCurrentRawStream(index))

@@ -328,7 +328,7 @@ def stream_error(workspace: torch.Tensor, num_shares: int, heads: int, kv_heads:
     return int(workspace[off:off + 4].view(torch.int32).item())
 
 
-_PIECES_WORKSPACES: dict = {}  # the pieces plans' workspaces, apart from the decode ones
+_PIECES_WORKSPACES: dict = {}  # the pieces plans' workspaces (a family apart from the decode ones)
 
 
 def pieces_workspace_bytes(num_slots: int, heads: int, head_dim: int) -> int:

@@ -83,9 +83,8 @@ class AttentionBackend:
     def _prefill_workspace(self, meta: AttnMetadata, q: torch.Tensor) -> torch.Tensor | None:
         """This backend's workspace for a prefill call in the verify form
         (the decode kernels) when it holds what the call needs, else None: the
-        call then takes the per-stream cached workspace. A PrefillPieces plan
-        never gets it: its slots start at the first byte, where a decode
-        workspace keeps the one-launch merge's counters."""
+        call then takes the per-stream cached workspace (a PrefillPieces plan
+        takes the pieces' own cached one)."""
         ws = self.decode_workspace
         if ws is None or meta.prefill_kernel != "verify":
             return None

@@ -66,12 +66,10 @@ def test_workspace_bytes_is_a_pure_size_formula():
     def want(b, h, d, maxc):
         waves = max(1, min(256 * 8, b * -(-maxc // 16) // 2))  # slices of >= 2 pages, <= resident waves
         slots = waves + b  # one per (wave, sequence) piece
-        # counters + error word, prefix, (m, l), O
-        return counters + r256((b + 1) * 4) + r256(slots * h * 2 * 4) + slots * h * d * 4
+        return r256((b + 1) * 4) + r256(slots * h * 2 * 4) + slots * h * d * 4  # prefix, (m, l), O
 
-    counters = 8192 * 4 + 256  # NIMBUS_DECODE_COUNTER_BYTES
-    assert f(64, 32, 128, 8192) == want(64, 32, 128, 8192) == counters + 512 + 2112 * 32 * 8 + 2112 * 32 * 512
-    assert f(1, 32, 128, 100) == want(1, 32, 128, 100) == counters + 256 + 1024 + 4 * 32 * 512  # 3 slices + 1
+    assert f(64, 32, 128, 8192) == want(64, 32, 128, 8192) == 512 + 2112 * 32 * 8 + 2112 * 32 * 512
+    assert f(1, 32, 128, 100) == want(1, 32, 128, 100) == 256 + 1024 + 4 * 32 * 512  # 7 pages: 3 slices + 1
     assert f(16, 32, 64, 1024) == want(16, 32, 64, 1024)
     assert f(-1, 32, 128, 8192) == -1
 
