@@ -270,9 +270,9 @@ def time_decode(batch, steps, warmup, wall=True):
         q, kc, vc = pools[i % len(pools)]
         paged_decode_attention(q[t0:], kc, vc, ctx, bt, maxc, batch.scale, out=out, workspace=ws, _entry=entry)
 
-    for i in range(warmup):
-        call(i)
-    torch.cuda.synchronize()
+    # (time-based: the first timed section of a process would otherwise meet cold clocks and first-launch costs)
+    warm_up(call, warmup)
+    warm_up(lambda i: call(i, "nimbus_paged_decode_pages"), 2)
     res = {}
     if wall:
         torch.cuda.synchronize()
