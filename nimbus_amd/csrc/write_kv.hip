@@ -24,16 +24,21 @@ struct WriteKVArgs {
   int32_t kv, d;
 };
 
+// PIECES: 16-byte pieces per head row (8 at head_dim 64, 16 at 128; 0 for any
+// other head_dim, read from the arguments). The host launches it only when
+// the piece count fits 32 bits, so the index arithmetic is 32-bit (a 64-bit
+// divide per piece cost more than the copy).
+template <int PIECES>
 __global__ __launch_bounds__(256) void write_kv_vec_kernel(WriteKVArgs a) {
-  const int pieces = a.d / 8;                       // 16-byte pieces per head row
-  const int64_t per_token = static_cast<int64_t>(a.kv) * pieces;
-  const int64_t total = a.n_tokens * per_token;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t t = i / per_token;
-    const int rem = static_cast<int>(i - t * per_token);
-    const int h = rem / pieces;
-    const int c = rem - h * pieces;
+  const uint32_t pieces = PIECES ? PIECES : a.d / 8;
+  const uint32_t per_token = static_cast<uint32_t>(a.kv) * pieces;
+  const uint32_t total = static_cast<uint32_t>(a.n_tokens) * per_token;
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+    const uint32_t t32 = i / per_token;
+    const uint32_t rem = i - t32 * per_token;
+    const int h = static_cast<int>(rem / pieces);
+    const int c = static_cast<int>(rem - h * pieces);
+    const int64_t t = t32;
     const int64_t slot = a.slots[t];
     if (slot < 0 || slot >= a.num_slots) continue;
     const u32x4 kv = *reinterpret_cast<const u32x4*>(a.k + t * a.k_st + h * a.k_sh + 8 * c);
@@ -117,8 +122,10 @@ extern "C" int nimbus_write_kv(const void* k, const void* v, void* k_cache, void
   int64_t blocks = (work + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (vec) {
-    hipLaunchKernelGGL(write_kv_vec_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+  if (vec && work < (int64_t{1} << 31)) {
+    if (head_dim == 128) hipLaunchKernelGGL(write_kv_vec_kernel<16>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    else if (head_dim == 64) hipLaunchKernelGGL(write_kv_vec_kernel<8>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL(write_kv_vec_kernel<0>, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
   } else {
     hipLaunchKernelGGL(write_kv_scalar_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, a);
   }
