@@ -25,6 +25,14 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Buffer resources (raw, unswizzled access with a 32-bit data format in
+// descriptor word 3) and the cache-policy bit of buffer loads and stores
+// that makes them agent-scope (sc1): they bypass the non-coherent L2 of the
+// issuing XCD, so data one XCD writes this way is seen by another reading
+// it this way once the write has completed.
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kSc1 = 16;
+
 // ---------------------------------------------------------------- conversions
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) {

@@ -44,7 +44,6 @@ constexpr int kMaxSplits = 16;
 constexpr int kMinSplitK = kGemmRing * kGemmStep;  // splits are whole rings of steps
 constexpr int kFillWorkgroups = 256;        // one per CU of a gfx950 part
 
-constexpr int32_t kBufferFlags = 0x00020000;     // raw buffer descriptor word 3 for gfx950
 constexpr uint32_t kOutOfRange = 0xFFFFFFF0u;     // a buffer offset past any operand: reads zero
 
 struct GemmArgs {

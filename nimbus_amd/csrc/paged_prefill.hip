@@ -53,7 +53,6 @@ namespace nimbus {
 
 constexpr int kBlockN = 64;        // keys per iteration (four pages)
 constexpr float kLazyMax = 8.f;    // log2 headroom before the running max moves
-constexpr int kBufferFlags = 0x00020000;  // buffer resource word 3: 32-bit data format, raw (unswizzled) access
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -611,7 +610,6 @@ __device__ __forceinline__ void prefill_unit() {
     // bypass the non-coherent L2 of the writer's and reader's XCDs; the
     // writer's flag for (slot, wave) goes out once its stores are complete.
     constexpr int SLOT_FLOATS = (ND * 16 + 2) * 64;  // per wave
-    constexpr int kSc1 = 16;                         // cache-policy bit: agent scope
     auto slot_rsrc = [&](int s) {
       float* base = a.sk_part + (static_cast<int64_t>(s) * Shape::kWaves + wave) * SLOT_FLOATS;
       return __builtin_amdgcn_make_buffer_rsrc(base, 0, SLOT_FLOATS * 4, kBufferFlags);
