@@ -42,7 +42,9 @@ mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
              rows read and written + slots, against 8 TB/s)
 verify       speculative verification's attention (16 sequences x 5 tokens)
              replayed from a hipGraph, with the decode kernel on the same
-             contexts beside it
+             contexts beside it; `attention_us_graph` and
+             `decode_same_contexts_us_graph` compare the two attention calls
+             alone (no slot write), each as back-to-back calls in a hipGraph
 add_rms_norm the fused residual add + RMSNorm at three model shapes:
              algorithmic bytes (x and residual read, residual and output
              written, weight once) / mean kernel time, against 8 TB/s
@@ -559,7 +561,8 @@ def time_verify(steps, warmup, n=16, k=4):
     from nimbus_amd import workloads
     from nimbus_amd.graphs import VerifyAttentionGraphs
     from nimbus_amd.kernels.paged_attention import (decode_workspace_bytes, new_decode_workspace,
-                                                    paged_decode_attention)
+                                                    paged_decode_attention, paged_verify_attention,
+                                                    verify_workspace_bytes)
 
     q_len = k + 1
     ctx = workloads.llama3_decode_lens(seed=7, batch=n)
@@ -589,13 +592,27 @@ def time_verify(steps, warmup, n=16, k=4):
     outd = torch.empty_like(qd)
     for _ in range(warmup):
         paged_decode_attention(qd, kc, vc, pa[4], b.block_tables, max(ctx), b.scale, out=outd, workspace=ws)
-    dus = statistics.mean(event_times_us(
-        lambda i: paged_decode_attention(qd, kc, vc, pa[4], b.block_tables, max(ctx), b.scale, out=outd,
-                                         workspace=ws), steps, torch.cuda.current_stream()))
+    def decode_call(i):
+        paged_decode_attention(qd, kc, vc, pa[4], b.block_tables, max(ctx), b.scale, out=outd, workspace=ws)
+
+    dus = statistics.mean(event_times_us(decode_call, steps, torch.cuda.current_stream()))
+    # Like for like: the verify attention call alone (no slot write) and the
+    # decode call, each captured back to back in a hipGraph.
+    wsv = new_decode_workspace(verify_workspace_bytes(n, q_len, 32, 128, 8192), torch.device("cuda"))
+    outv = torch.empty_like(b.q)
+
+    def verify_call(i):
+        paged_verify_attention(b.q, kc, vc, pa[4], b.block_tables, q_len, 8192, b.scale, out=outv, workspace=wsv)
+
+    warm_up(verify_call, warmup)
+    stream = torch.cuda.current_stream()
+    vg = graph_us(verify_call, 12, stream)
+    dg = graph_us(decode_call, 12, stream)
     return {"workload": f"{n} sequences x {q_len} tokens (k={k}), Llama-3-8B shape, contexts log-uniform "
                         f"[128, 8192] (sum {sum(ctx)})", "us_per_replay": us, "bytes": nbytes,
             "GBps": nbytes / us / 1e3, "tile_kernel_us_per_replay": times["tile"], "decode_same_contexts_us": dus,
-            "decode_same_contexts_GBps": (kv_bytes + 2 * n * 32 * 128 * 2) / dus / 1e3}
+            "decode_same_contexts_GBps": (kv_bytes + 2 * n * 32 * 128 * 2) / dus / 1e3,
+            "attention_us_graph": vg, "decode_same_contexts_us_graph": dg, "attention_over_decode": vg / dg}
 
 
 # ---------------------------------------------------------------- fused residual add + RMSNorm
@@ -1028,6 +1045,14 @@ def config_summary(result):
     if c5:
         out["config5_decode"] = {"us": r4(c5["us_per_call"]), "us_graph": r4(c5["us_per_call_graph"]),
                                  "frac_hbm": r4(c5["frac_hbm_peak_call"])}
+    for row in result.get("prefill_scaling") or []:
+        if row["workload"].startswith("one 8192"):
+            out["prompt8192_prefill"] = {"us": r4(row["us_per_call"]), "frac_mfma": r4(row["frac_mfma_peak"])}
+    v = result.get("verify")
+    if v:
+        out["verify_attention"] = {"us_graph": r4(v["attention_us_graph"]),
+                                   "decode_us_graph": r4(v["decode_same_contexts_us_graph"]),
+                                   "over_decode": r4(v["attention_over_decode"])}
     return out
 
 

@@ -8,7 +8,8 @@ prefill bar: within 2e-3 + 1e-2 |ref| of the oracle's fp32-accumulated
 attention. Cases: the query run inside one page and across a page edge,
 contexts that equal q_len (a fresh short prompt), sequences long enough that
 their pages are split between waves (the merge pass), GQA groups 1..8 with
-one and two 16-column chunks, both dtypes and head dims.
+one and two 16-column chunks (two chunks in workgroups of 2, 4, 5, 6 and 8
+waves), both dtypes and head dims.
 """
 
 from __future__ import annotations
@@ -43,6 +44,12 @@ CASES = [
     (8, 8, 64, 16, [16, 17, 40, 1500]),                       # MHA, a whole page of queries
     (12, 4, 64, 3, [3, 9, 700, 5000, 6]),                     # G = 3: 9 columns, a ragged chunk
     (16, 2, 128, 2, [2, 18, 33, 8000]),                       # G = 8: 16 columns
+    # two chunks with the chip filled, workgroups of 4, 6 and 2 waves holding both chunks of their kv heads,
+    # and 5-wave workgroups (10 kv groups), which keep a workgroup per chunk
+    (16, 2, 64, 3, [3, 40, 4200, 700]),
+    (24, 3, 64, 3, [3, 4000, 90]),
+    (8, 1, 128, 3, [17000, 3]),
+    (20, 5, 64, 5, [5, 2500, 600]),
 ]
 
 
