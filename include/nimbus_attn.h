@@ -16,9 +16,14 @@
  * before launch, or a positive hipError_t from the launch itself.
  *
  * Caches are [num_blocks, block_size, num_kv_heads, head_dim] with unit
- * stride in the last dimension (nimbus/cache/kv_cache.py:18-25);
- * block_size must be 16 and head_dim 64 or 128. Context lengths and block
- * tables are int32, slot mappings int64 (nimbus/runner.py:77-85).
+ * stride in the last dimension (nimbus/cache/kv_cache.py:18-25). The
+ * attention kernels are tuned for block_size 16 and head_dim 64 or 128; any
+ * other block_size >= 1 and head_dim 1..256 runs a general kernel (correct,
+ * not tuned; element loads, so no stride alignment asked and no workspace
+ * read) through the same entry points, except the two-pass decode entries
+ * and the prefill pieces and stream-K forms, which refuse such shapes with
+ * NIMBUS_ERR_UNSUPPORTED. Context lengths and block tables are int32, slot
+ * mappings int64 (nimbus/runner.py:77-85).
  */
 #ifndef NIMBUS_ATTN_H
 #define NIMBUS_ATTN_H
@@ -29,7 +34,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 12
+#define NIMBUS_ATTN_ABI_VERSION 13
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0

@@ -25,8 +25,8 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_NAME = "libnimbus_attn.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["write_kv.hip", "paged_decode.hip", "paged_prefill.hip", "rmsnorm.hip", "int8_matmul.hip",
-           "elementwise.hip"]
+SOURCES = ["write_kv.hip", "paged_decode.hip", "paged_prefill.hip", "paged_general.hip", "rmsnorm.hip",
+           "int8_matmul.hip", "elementwise.hip"]
 ARCH = "gfx950"
 
 

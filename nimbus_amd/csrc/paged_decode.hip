@@ -777,13 +777,49 @@ static int paged_decode_impl(int phases, int32_t nq, const void* q, int64_t q_st
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return NIMBUS_ERR_INVALID;
   if (nq <= 0) return NIMBUS_ERR_INVALID;
   if (nq > kMaxVerifyQueries) return NIMBUS_ERR_UNSUPPORTED;
-  if (block_size != kPage) return NIMBUS_ERR_UNSUPPORTED;
-  if (head_dim != 64 && head_dim != 128) return NIMBUS_ERR_UNSUPPORTED;
+  // Pages of other than 16 tokens and head dims other than 64 and 128 take
+  // the general kernel (paged_general.hip).
+  const bool general = general_shape(head_dim, block_size);
+  if (general) {
+    const int rc = general_check(head_dim, block_size);
+    if (rc != 0) return rc;
+  }
   if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
   if (batch > kMaxDecodeBatch || max_context > (int64_t{1} << 30)) return NIMBUS_ERR_UNSUPPORTED;
   if (batch == 0 || max_context <= 0) return NIMBUS_OK;
   if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !out) return NIMBUS_ERR_INVALID;
   if (num_blocks <= 0 || num_blocks > INT32_MAX || bt_width <= 0) return NIMBUS_ERR_INVALID;
+  if (general) {
+    // (element loads: no alignment asked of the strides; no workspace used)
+    if (phases != 3) return NIMBUS_ERR_UNSUPPORTED;  // one launch: there are no pieces to merge
+    AttnGeneralArgs g{};
+    g.q = static_cast<const uint16_t*>(q);
+    g.q_st = q_stride_b;
+    g.q_sh = q_stride_h;
+    g.kc = static_cast<const uint16_t*>(k_cache);
+    g.vc = static_cast<const uint16_t*>(v_cache);
+    g.c_sb = cache_stride_block;
+    g.c_st = cache_stride_token;
+    g.c_sh = cache_stride_head;
+    g.bt = block_tables;
+    g.bt_sb = bt_stride;
+    g.bt_width = bt_width;
+    g.num_blocks = static_cast<int32_t>(num_blocks);
+    g.bs = block_size;
+    g.ctx = context_lens;
+    g.nq = nq;
+    g.max_ctx = static_cast<int32_t>(max_context);
+    g.out = static_cast<uint16_t*>(out);
+    g.o_st = out_stride_b;
+    g.o_sh = out_stride_h;
+    g.H = num_heads;
+    g.G = num_heads / num_kv_heads;
+    g.KV = num_kv_heads;
+    g.D = head_dim;
+    g.scale_log2 = scale * 1.4426950408889634f;
+    if (static_cast<int64_t>(bt_width) * block_size > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
+    return launch_general_decode(g, batch, dtype, static_cast<hipStream_t>(stream));
+  }
   // 16-byte vector access: 8-element aligned strides and bases.
   if ((q_stride_b | q_stride_h | cache_stride_block | cache_stride_token | cache_stride_head | out_stride_b |
        out_stride_h) % 8 != 0)

@@ -851,9 +851,48 @@ static int prefill_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
                         const int32_t* sk_piece = nullptr) {
   if (num_units < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0)
     return NIMBUS_ERR_INVALID;
-  if (block_size != 16) return NIMBUS_ERR_UNSUPPORTED;
-  if (head_dim != 64 && head_dim != 128) return NIMBUS_ERR_UNSUPPORTED;
   if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  // Pages of other than 16 tokens and head dims other than 64 and 128 take
+  // the general kernel (paged_general.hip), over the plain tile table.
+  if (general_shape(head_dim, block_size)) {
+    const int rc = general_check(head_dim, block_size);
+    if (rc != 0) return rc;
+    if (pieces || sk_start) return NIMBUS_ERR_UNSUPPORTED;
+    if (num_units == 0) return NIMBUS_OK;
+    if (!q || !k_cache || !v_cache || !block_tables || !query_start || !context_lens || !out || !prog_seq ||
+        !prog_m)
+      return NIMBUS_ERR_INVALID;
+    if (num_blocks <= 0 || num_blocks > INT32_MAX || bt_width <= 0) return NIMBUS_ERR_INVALID;
+    if (static_cast<int64_t>(bt_width) * block_size > INT32_MAX) return NIMBUS_ERR_UNSUPPORTED;
+    AttnGeneralArgs g{};
+    g.q = static_cast<const uint16_t*>(q);
+    g.q_st = q_stride_t;
+    g.q_sh = q_stride_h;
+    g.kc = static_cast<const uint16_t*>(k_cache);
+    g.vc = static_cast<const uint16_t*>(v_cache);
+    g.c_sb = cache_stride_block;
+    g.c_st = cache_stride_token;
+    g.c_sh = cache_stride_head;
+    g.bt = block_tables;
+    g.bt_sb = bt_stride;
+    g.bt_width = bt_width;
+    g.num_blocks = static_cast<int32_t>(num_blocks);
+    g.bs = block_size;
+    g.ctx = context_lens;
+    g.qstart = query_start;
+    g.prog_seq = prog_seq;
+    g.prog_m = prog_m;
+    g.tile_pos = kPrefillTile;
+    g.out = static_cast<uint16_t*>(out);
+    g.o_st = out_stride_t;
+    g.o_sh = out_stride_h;
+    g.H = num_heads;
+    g.G = num_heads / num_kv_heads;
+    g.KV = num_kv_heads;
+    g.D = head_dim;
+    g.scale_log2 = scale * 1.4426950408889634f;
+    return launch_general_prefill(g, num_units, dtype, static_cast<hipStream_t>(stream));
+  }
   const int G = num_heads / num_kv_heads;
   // Heads per unit: the largest of 8, 4, 2, 1 that divides G.
   const int gs = G % 8 == 0 ? 8 : (G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1));

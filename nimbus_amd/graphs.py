@@ -40,7 +40,7 @@ import numpy as np
 import torch
 
 from nimbus_amd.kernels.elementwise import greedy_step
-from nimbus_amd.kernels.paged_attention import (PAGE, decode_workspace_bytes, new_decode_workspace,
+from nimbus_amd.kernels.paged_attention import (decode_workspace_bytes, new_decode_workspace,
                                                 verify_workspace_bytes)
 from nimbus_amd.kernels.prefill_attention import verify_queries
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
@@ -194,7 +194,7 @@ class VerifyAttentionGraphs:
         workspace = None
         if kernel == "auto" and verify_queries(list(range(0, (max_batch + 1) * q, q)), num_heads, kv):
             # the verify form bounds contexts by the block-table width
-            nbytes = verify_workspace_bytes(max_batch, q, num_heads, d, width * PAGE)
+            nbytes = verify_workspace_bytes(max_batch, q, num_heads, d, width * self.block_size)
             workspace = new_decode_workspace(nbytes, dev)
         self.backend = AttentionBackend(decode_workspace=workspace)
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata]] = {}
@@ -481,7 +481,7 @@ class VerifyGraphs:
         self.workspace = None
         if kernel == "auto" and verify_queries(list(range(0, (max_batch + 1) * q, q)), cfg.num_heads,
                                                cfg.num_kv_heads):
-            need = verify_workspace_bytes(max_batch, q, cfg.num_heads, cfg.head_dim, width * PAGE)
+            need = verify_workspace_bytes(max_batch, q, cfg.num_heads, cfg.head_dim, width * block_size)
             self.workspace = new_decode_workspace(need, device)
         self.graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, AttnMetadata]] = {}
 

@@ -20,7 +20,7 @@ import torch
 from nimbus_amd import _lib
 from nimbus_amd.kernels import index_checks
 
-PAGE = 16  # tokens per KV-cache block: the only block size the kernels take
+PAGE = 16  # tokens per KV-cache block of the tuned kernels (other sizes run the general kernel)
 
 
 def decode_workspace_bytes(batch: int, heads: int, head_dim: int, max_context: int) -> int:

@@ -23,7 +23,7 @@ import torch
 
 from nimbus_amd import _lib
 from nimbus_amd.kernels import index_checks
-from nimbus_amd.kernels.paged_attention import (MAX_VERIFY_QUERIES, PAGE, _cached_workspace, _check_cache,
+from nimbus_amd.kernels.paged_attention import (MAX_VERIFY_QUERIES, _cached_workspace, _check_cache,
                                                 paged_verify_attention)
 
 BLOCK_M = 64  # query positions per tile-table entry (NIMBUS_PREFILL_TILE)
@@ -394,7 +394,7 @@ def paged_prefill_attention(
                          f"{VERIFY_MAX_COLUMNS} columns per kv group")
     if nq:
         return paged_verify_attention(q, k_cache, v_cache, context_lens, block_tables, nq,
-                                      block_tables.shape[1] * PAGE, scale, out=out, workspace=workspace)
+                                      block_tables.shape[1] * k_cache.shape[1], scale, out=out, workspace=workspace)
     if index_checks.enabled():
         index_checks.check_tables(block_tables, context_lens, k_cache.shape[0], k_cache.shape[1])
     if programs is None:

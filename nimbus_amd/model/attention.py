@@ -80,7 +80,7 @@ class AttentionBackend:
         self._prefill = prefill_attention.paged_prefill_attention
         self._build_programs = prefill_attention.build_programs
 
-    def _prefill_workspace(self, meta: AttnMetadata, q: torch.Tensor) -> torch.Tensor | None:
+    def _prefill_workspace(self, meta: AttnMetadata, q: torch.Tensor, block_size: int) -> torch.Tensor | None:
         """This backend's workspace for a prefill call in the verify form
         (the decode kernels) when it holds what the call needs, else None: the
         call then takes the per-stream cached workspace (a PrefillPieces plan
@@ -90,7 +90,7 @@ class AttentionBackend:
             return None
         h, d = q.shape[1], q.shape[2]
         need = paged_attention.verify_workspace_bytes(meta.num_prefills, meta.prefill_query_start_host[1], h, d,
-                                                      meta.prefill_block_tables.shape[1] * paged_attention.PAGE)
+                                                      meta.prefill_block_tables.shape[1] * block_size)
         return ws if ws.numel() * ws.element_size() >= need else None
 
     def forward(
@@ -129,7 +129,7 @@ class AttentionBackend:
                 q[:p], k_cache, v_cache, meta.prefill_query_start, meta.prefill_context_lens,
                 meta.prefill_block_tables, scale, meta.prefill_query_start_host,
                 meta.prefill_context_lens_host, meta.prefill_programs, out=out[:p],
-                workspace=self._prefill_workspace(meta, q), kernel=meta.prefill_kernel,
+                workspace=self._prefill_workspace(meta, q, k_cache.shape[1]), kernel=meta.prefill_kernel,
             )
         if meta.num_decodes:
             self._decode(

@@ -30,8 +30,9 @@ def compact(k_cache, v_cache, block_tables, ctx_lens_host):
     """Copies the pages the rows use to small CPU caches; returns
     (k, v, tables) with tables renumbered into them (zero padded)."""
     rows, lens = [], []
+    bs = k_cache.shape[1]
     for b, c in enumerate(ctx_lens_host):
-        n = -(-int(c) // 16)
+        n = -(-int(c) // bs)
         rows.append(block_tables[b, :n].long())
         lens.append(n)
     used = torch.cat(rows) if rows else torch.zeros(0, dtype=torch.long, device=block_tables.device)

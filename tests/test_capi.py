@@ -98,8 +98,12 @@ def _decode(**kw):
 
 
 @pytest.mark.parametrize("kw,code", [
-    (dict(bs=8), _lib.NIMBUS_ERR_UNSUPPORTED),
-    (dict(d=96), _lib.NIMBUS_ERR_UNSUPPORTED),
+    # other page sizes and head dims run the general kernel; past it they are refused before launch
+    (dict(bs=0), _lib.NIMBUS_ERR_UNSUPPORTED),
+    (dict(d=264), _lib.NIMBUS_ERR_UNSUPPORTED),
+    (dict(d=96, bs=8, q=None), _lib.NIMBUS_ERR_INVALID),
+    (dict(d=96, bs=8, b=0), 0),
+    (dict(d=96, bs=8, dt=7), _lib.NIMBUS_ERR_UNSUPPORTED),
     (dict(dt=7), _lib.NIMBUS_ERR_UNSUPPORTED),
     (dict(h=30), _lib.NIMBUS_ERR_INVALID),
     (dict(q=None), _lib.NIMBUS_ERR_INVALID),
@@ -129,7 +133,8 @@ def test_verify_argument_checks():
 
     assert verify(0) == _lib.NIMBUS_ERR_INVALID
     assert verify(17) == _lib.NIMBUS_ERR_UNSUPPORTED
-    assert verify(5, bs=8) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert verify(5, bs=0) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert verify(5, d=264) == _lib.NIMBUS_ERR_UNSUPPORTED
     assert verify(5, b=0) == 0
     # a workspace big enough for decode is too small for five query columns
     dec = lib.nimbus_paged_decode_workspace_bytes(2, 32, 128, 64)
@@ -140,9 +145,12 @@ def test_prefill_and_write_kv_argument_checks():
     lib = _lib.load()
     base = [DUMMY, 32 * 128, 128, DUMMY, DUMMY, 100, 16 * 8 * 128, 8 * 128, 128, DUMMY, 4, 4, DUMMY, DUMMY, DUMMY,
             DUMMY, 3, DUMMY, 32 * 128, 128, 32, 8, 128, 16, 0.1, 1, None]
-    assert lib.nimbus_paged_prefill(*base[:23], 8, *base[24:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # block size
+    # other page sizes and head dims run the general kernel; past it they are refused before launch
+    assert lib.nimbus_paged_prefill(*base[:23], 0, *base[24:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # block size
     assert lib.nimbus_paged_prefill(*base[:16], 0, *base[17:]) == 0  # no tiles: nothing to launch
-    assert lib.nimbus_paged_prefill(*base[:22], 80, *base[23:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # head dim
+    assert lib.nimbus_paged_prefill(*base[:22], 264, *base[23:]) == _lib.NIMBUS_ERR_UNSUPPORTED  # head dim
+    assert lib.nimbus_paged_prefill(*base[:22], 80, 8, *base[24:25], 7, None) == _lib.NIMBUS_ERR_UNSUPPORTED  # dtype
+    assert lib.nimbus_paged_prefill(*base[:16], 0, *base[17:22], 80, 8, *base[24:]) == 0  # general, no tiles
     # page offsets are 32 x 32-bit products: block strides of 2^30 elements and up are refused
     assert lib.nimbus_paged_prefill(*base[:6], 1 << 30, *base[7:]) == _lib.NIMBUS_ERR_UNSUPPORTED
     wk =[DUMMY, DUMMY, DUMMY, DUMMY, DUMMY, 0, 8, 128, 8 * 128, 128, 8 * 128, 128, 1600, 1, None]

@@ -1,0 +1,126 @@
+"""GPU: page sizes other than 16 and head dims other than 64 and 128.
+
+The reference's Triton kernels take BLOCK_SIZE = k_cache.shape[1] and any
+power-of-two head dim (nimbus/kernels/paged_attention.py:139-140,
+nimbus/kernels/prefill_attention.py:115); here those shapes run the general
+kernel (nimbus_amd/csrc/paged_general.hip) through the same entry points.
+Decode, verify and varlen prefill calls are checked against the oracle
+(which gathers pages by the cache's own block size) within
+2e-3 + 1e-2 |ref|, at pages of 1, 8 and 32 tokens and head dims 32, 80, 96
+and 256 (and 128 on 32-token pages), GQA groups 1-8, both dtypes; contexts
+at and around page edges, rows longer than the block table covers cut to
+it, and a graph-captured decode call that replays bit for bit.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nimbus_amd.kernels.paged_attention import paged_decode_attention, paged_verify_attention
+from nimbus_amd.kernels.prefill_attention import paged_prefill_attention
+from tests.gpu_helpers import announce, oracle_decode, oracle_prefill
+from tests.helpers import assert_within, query_starts, random_tables, scattered_cache
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # heads, kv, head dim, block size
+    (32, 8, 96, 16),
+    (16, 4, 256, 16),
+    (8, 8, 32, 32),
+    (12, 4, 80, 8),
+    (32, 8, 128, 32),
+    (4, 1, 64, 1),
+]
+
+
+def _cache(kv, d, bs, ctx_lens, dtype, seed):
+    pool = sum(-(-c // bs) for c in ctx_lens) + 4
+    k, v = scattered_cache(pool, bs, kv, d, seed=seed, dtype=dtype, device="cuda")
+    bt = random_tables(ctx_lens, bs, pool, seed=seed, device="cuda")
+    return k, v, bt
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("heads,kv,d,bs", SHAPES)
+def test_general_decode_matches_oracle(dtype, heads, kv, d, bs):
+    ctx_lens = [1, bs, bs + 1, 2 * bs - 1, 700, 3000]
+    announce(f"general decode H={heads} KV={kv} D={d} bs={bs} {dtype}")
+    k, v, bt = _cache(kv, d, bs, ctx_lens, dtype, seed=d + bs)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn(len(ctx_lens), heads, d, generator=g, device="cuda").to(dtype)
+    ctx = torch.tensor(ctx_lens, dtype=torch.int32, device="cuda")
+    got = paged_decode_attention(q, k, v, ctx, bt, max(ctx_lens), d ** -0.5)
+    torch.cuda.synchronize()
+    assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, d ** -0.5), what="general decode vs oracle")
+
+
+@pytest.mark.parametrize("heads,kv,d,bs", [(32, 8, 96, 32), (12, 4, 256, 8)])
+def test_general_verify_matches_oracle(heads, kv, d, bs):
+    nq = 3
+    ctx_lens = [3, bs + 2, 900, 2500]
+    announce(f"general verify H={heads} KV={kv} D={d} bs={bs} nq={nq}")
+    k, v, bt = _cache(kv, d, bs, ctx_lens, torch.bfloat16, seed=11)
+    qs = query_starts([nq] * len(ctx_lens))
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q = torch.randn(qs[-1], heads, d, generator=g, device="cuda").bfloat16()
+    ctx = torch.tensor(ctx_lens, dtype=torch.int32, device="cuda")
+    got = paged_verify_attention(q, k, v, ctx, bt, nq, max(ctx_lens), d ** -0.5)
+    routed = paged_prefill_attention(q, k, v, torch.tensor(qs, dtype=torch.int32, device="cuda"), ctx, bt,
+                                     d ** -0.5, qs, ctx_lens)
+    tile = paged_prefill_attention(q, k, v, torch.tensor(qs, dtype=torch.int32, device="cuda"), ctx, bt,
+                                   d ** -0.5, qs, ctx_lens, kernel="tile")
+    torch.cuda.synchronize()
+    want = oracle_prefill(q, k, v, qs, ctx_lens, bt, d ** -0.5)
+    assert_within(got.cpu(), want, what="general verify vs oracle")
+    assert_within(routed.cpu(), want, what="routed prefill call vs oracle")
+    assert_within(tile.cpu(), want, what="tile-table prefill vs oracle")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("heads,kv,d,bs", [(32, 8, 96, 32), (16, 2, 256, 8), (8, 8, 32, 1), (32, 8, 128, 32)])
+def test_general_prefill_matches_oracle(dtype, heads, kv, d, bs):
+    """Varlen causal chunks on cached prefixes, the chunks 1-200 tokens (more
+    than one 64-position tile), a fresh prompt and a chunk on a long prefix."""
+    q_lens = [1, 70, 200, 5, 64]
+    prefixes = [0, 33, 500, 1200, 0]
+    ctx_lens = [a + b for a, b in zip(q_lens, prefixes)]
+    announce(f"general prefill H={heads} KV={kv} D={d} bs={bs} {dtype}")
+    k, v, bt = _cache(kv, d, bs, ctx_lens, dtype, seed=5)
+    qs = query_starts(q_lens)
+    g = torch.Generator(device="cuda").manual_seed(6)
+    q = torch.randn(qs[-1], heads, d, generator=g, device="cuda").to(dtype)
+    ctx = torch.tensor(ctx_lens, dtype=torch.int32, device="cuda")
+    got = paged_prefill_attention(q, k, v, torch.tensor(qs, dtype=torch.int32, device="cuda"), ctx, bt,
+                                  d ** -0.5, qs, ctx_lens)
+    torch.cuda.synchronize()
+    assert_within(got.cpu(), oracle_prefill(q, k, v, qs, ctx_lens, bt, d ** -0.5), what="general prefill vs oracle")
+
+
+def test_general_decode_cut_to_table_and_graph_replay():
+    """max_context and the block table's width bound the keys read (a context
+    past them is cut, as in the tuned kernels); a graph-captured call replays
+    bit for bit."""
+    heads, kv, d, bs = 16, 4, 96, 8
+    ctx_lens = [40, 90, 7]
+    announce("general decode bounds and graph replay")
+    k, v, bt = _cache(kv, d, bs, ctx_lens, torch.bfloat16, seed=9)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    q = torch.randn(len(ctx_lens), heads, d, generator=g, device="cuda").bfloat16()
+    ctx = torch.tensor(ctx_lens, dtype=torch.int32, device="cuda")
+    cut = paged_decode_attention(q, k, v, ctx, bt, 48, d ** -0.5)  # max_context 48: the 90-token row sees 48
+    want = oracle_decode(q, k, v, [40, 48, 7], bt, d ** -0.5)
+    assert_within(cut.cpu(), want, what="cut to max_context")
+    out = torch.empty_like(q)
+    eager = paged_decode_attention(q, k, v, ctx, bt, 96, d ** -0.5)
+    paged_decode_attention(q, k, v, ctx, bt, 96, d ** -0.5, out=out)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        paged_decode_attention(q, k, v, ctx, bt, 96, d ** -0.5, out=out)
+    for _ in range(3):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
