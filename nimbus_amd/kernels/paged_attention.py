@@ -23,6 +23,13 @@ from nimbus_amd.kernels import index_checks
 PAGE = 16  # tokens per KV-cache block of the tuned kernels (other sizes run the general kernel)
 
 
+def tuned_shape(block_size: int, head_dim: int) -> bool:
+    """Whether the tuned kernels take this page size and head dim; other
+    shapes run the general kernel, which has no prefill pieces or stream-K
+    form."""
+    return block_size == PAGE and head_dim in (64, 128)
+
+
 def decode_workspace_bytes(batch: int, heads: int, head_dim: int, max_context: int) -> int:
     return int(_lib.load().nimbus_paged_decode_workspace_bytes(batch, heads, head_dim, max_context))
 

@@ -120,11 +120,15 @@ class AttentionBackend:
                 meta.prefill_kernel = "verify" if nq else "tile"
             if meta.prefill_programs is None and meta.prefill_kernel == "tile":
                 # Heavy tiles' key ranges cut into pieces when the tiles alone
-                # would not fill the chip, else the cost-ordered tile table.
-                meta.prefill_programs = prefill_attention.plan_pieces(
-                    meta.prefill_query_start_host, meta.prefill_context_lens_host, q.shape[1], k_cache.shape[2],
-                    q.device) or self._build_programs(meta.prefill_query_start_host, q.device,
-                                                      meta.prefill_context_lens_host)
+                # would not fill the chip, else the cost-ordered tile table
+                # (always the table for shapes the general kernel runs).
+                pieces = None
+                if paged_attention.tuned_shape(k_cache.shape[1], q.shape[2]):
+                    pieces = prefill_attention.plan_pieces(meta.prefill_query_start_host,
+                                                           meta.prefill_context_lens_host, q.shape[1],
+                                                           k_cache.shape[2], q.device)
+                meta.prefill_programs = pieces or self._build_programs(meta.prefill_query_start_host, q.device,
+                                                                       meta.prefill_context_lens_host)
             self._prefill(
                 q[:p], k_cache, v_cache, meta.prefill_query_start, meta.prefill_context_lens,
                 meta.prefill_block_tables, scale, meta.prefill_query_start_host,

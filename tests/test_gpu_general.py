@@ -124,3 +124,56 @@ def test_general_decode_cut_to_table_and_graph_replay():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager)
+
+
+def test_backend_step_on_32_token_pages():
+    """A flat step (prefill chunks then decodes, as runner.prepare lays it
+    out) through AttentionBackend.forward on 32-token pages and D = 96: the
+    slot write (any page size: a flat slot view) is bit-exact and both
+    attention parts match the oracle."""
+    from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
+
+    heads, kv, d, bs = 16, 4, 96, 32
+    prefills = [(100, 40), (0, 5)]  # (cached prefix, new tokens)
+    decodes = [300, 65, 1]           # context lengths, the newest token included
+    ctx_all = [p + q for p, q in prefills] + decodes
+    announce("general backend step bs=32 D=96")
+    k_cache, v_cache, bt = _cache(kv, d, bs, ctx_all, torch.bfloat16, seed=12)
+    bt_host = bt.cpu()
+    positions, rows = [], []
+    for s, (p, q) in enumerate(prefills):
+        positions += list(range(p, p + q))
+        rows += [s] * q
+    for s, c in enumerate(decodes, start=len(prefills)):
+        positions.append(c - 1)
+        rows.append(s)
+    slots = torch.tensor([int(bt_host[r, pos // bs]) * bs + pos % bs for r, pos in zip(rows, positions)],
+                         dtype=torch.int64, device="cuda")
+    t = len(positions)
+    g = torch.Generator(device="cuda").manual_seed(13)
+    q = torch.randn(t, heads, d, generator=g, device="cuda").bfloat16()
+    k_new = torch.randn(t, kv, d, generator=g, device="cuda").bfloat16()
+    v_new = torch.randn(t, kv, d, generator=g, device="cuda").bfloat16()
+    qs_host = [0]
+    for _, n in prefills:
+        qs_host.append(qs_host[-1] + n)
+    ctx_pre = [p + n for p, n in prefills]
+    n_pre = qs_host[-1]
+    meta = AttnMetadata(
+        slot_mapping=slots, num_prefill_tokens=n_pre,
+        prefill_query_start=torch.tensor(qs_host, dtype=torch.int32, device="cuda"),
+        prefill_context_lens=torch.tensor(ctx_pre, dtype=torch.int32, device="cuda"),
+        prefill_block_tables=bt[:len(prefills)],
+        decode_context_lens=torch.tensor(decodes, dtype=torch.int32, device="cuda"),
+        decode_block_tables=bt[len(prefills):], max_decode_context=max(decodes),
+        prefill_query_start_host=qs_host, prefill_context_lens_host=ctx_pre)
+    k_before = k_cache.clone()
+    out = AttentionBackend().forward(q, k_new, v_new, k_cache, v_cache, meta, d ** -0.5)
+    torch.cuda.synchronize()
+    kref = k_before.view(-1, kv, d)
+    kref[slots] = k_new
+    assert torch.equal(k_cache.view(-1, kv, d).view(torch.int16), kref.view(torch.int16))
+    assert_within(out[:n_pre].cpu(), oracle_prefill(q[:n_pre], k_cache, v_cache, qs_host, ctx_pre,
+                                                    bt[:len(prefills)], d ** -0.5), what="prefill part")
+    assert_within(out[n_pre:].cpu(), oracle_decode(q[n_pre:], k_cache, v_cache, decodes, bt[len(prefills):],
+                                                   d ** -0.5), what="decode part")
