@@ -680,7 +680,7 @@ template <int DT, int BM>
 static int launch_packed_bm(const GemmArgs& a, int ks, int rw, hipStream_t s) {
   switch (ks) {
     case 1: return launch_packed_rw<DT, BM, 1>(a, rw, s);
-    case 2: return launch_packed_rw<DT, BM, 2>(a, rw, s);
+    case 2: if constexpr (BM <= 64) return launch_packed_rw<DT, BM, 2>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
     case 4: if constexpr (BM <= 32) return launch_packed_rw<DT, BM, 4>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
     default: if constexpr (BM <= 16) return launch_packed_rw<DT, BM, 8>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
   }
@@ -691,6 +691,7 @@ static int launch_packed_dt(const GemmArgs& a, const PackPlan& p, hipStream_t s)
   switch (p.bm) {
     case 16: return launch_packed_bm<DT, 16>(a, p.ks, p.rw, s);
     case 32: return launch_packed_bm<DT, 32>(a, p.ks, p.rw, s);
+    case 128: return launch_packed_bm<DT, 128>(a, p.ks, p.rw, s);
     default: return launch_packed_bm<DT, 64>(a, p.ks, p.rw, s);
   }
 }
@@ -913,15 +914,15 @@ extern "C" int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const 
                      stream);
 }
 
-// An explicit plan: token tile bm (16, 32, 64), k slices ks (1, 2, 4, 8;
-// ks * bm <= 128), k splits (1..16, fewer when K is short) and row blocks
+// An explicit plan: token tile bm (16, 32, 64, 128), k slices ks (1, 2, 4,
+// 8; ks * bm <= 128), k splits (1..16, fewer when K is short) and row blocks
 // per wave rw (1, 2). Workspace: splits * m * n * 4 bytes when the plan
 // splits.
 static bool make_plan(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks, int32_t splits, int32_t rw,
                       PackPlan* p) {
   (void)m;
   (void)n;
-  if (bm != 16 && bm != 32 && bm != 64) return false;
+  if (bm != 16 && bm != 32 && bm != 64 && bm != 128) return false;
   if (ks != 1 && ks != 2 && ks != 4 && ks != 8) return false;
   if (rw != 1 && rw != 2) return false;
   if (ks * bm > 128 || splits < 1 || splits > kMaxSplits) return false;

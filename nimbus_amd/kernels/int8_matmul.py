@@ -120,7 +120,7 @@ def m_bucket(m: int) -> int:
 def _candidate_plans(m: int, n: int, k: int) -> list[tuple[int, int, int, int]]:
     nb = -(-n // 16)
     plans = []
-    for bm in (16, 32, 64):
+    for bm in (16, 32, 64, 128):
         if bm > 16 and m <= bm // 2:
             continue  # a smaller tile covers M
         for ks in (1, 2, 4, 8):

@@ -209,7 +209,8 @@ def test_pack_unpack_roundtrip_and_layout(n, k):
     assert int(pc[nb, kc, 16 * lane + e]) == want
 
 
-@pytest.mark.parametrize("m,n,k", [(33, 4100, 1040), (64, 4096, 4096), (7, 6144, 4096), (1, 260, 8192)])
+@pytest.mark.parametrize("m,n,k", [(33, 4100, 1040), (64, 4096, 4096), (7, 6144, 4096), (1, 260, 8192),
+                                   (200, 2080, 1040)])
 def test_every_launch_plan_is_exact(m, n, k):
     """Each plan the tuner may pick (token tile, k slices, K splits, row
     blocks per wave) gives
