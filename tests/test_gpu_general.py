@@ -7,7 +7,8 @@ kernel (nimbus_amd/csrc/paged_general.hip) through the same entry points.
 Decode, verify and varlen prefill calls are checked against the oracle
 (which gathers pages by the cache's own block size) within
 2e-3 + 1e-2 |ref|, at pages of 1, 8 and 32 tokens and head dims 32, 80, 96
-and 256 (and 128 on 32-token pages), GQA groups 1-8, both dtypes; contexts
+and 256 (and 128 on 32-token pages), GQA groups 1-32 (at 32 the heads of a
+kv head split over several workgroups), both dtypes; contexts
 at and around page edges, rows longer than the block table covers cut to
 it, and a graph-captured decode call that replays bit for bit.
 """
@@ -32,6 +33,8 @@ SHAPES = [
     (12, 4, 80, 8),
     (32, 8, 128, 32),
     (4, 1, 64, 1),
+    (32, 1, 256, 8),    # G = 32 at D = 256: four workgroups of 8 heads per kv head
+    (64, 2, 96, 16),    # G = 32 at D = 96: two chunks, 21 + 11 heads
 ]
 
 
@@ -56,7 +59,7 @@ def test_general_decode_matches_oracle(dtype, heads, kv, d, bs):
     assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, d ** -0.5), what="general decode vs oracle")
 
 
-@pytest.mark.parametrize("heads,kv,d,bs", [(32, 8, 96, 32), (12, 4, 256, 8)])
+@pytest.mark.parametrize("heads,kv,d,bs", [(32, 8, 96, 32), (12, 4, 256, 8), (32, 1, 256, 16)])
 def test_general_verify_matches_oracle(heads, kv, d, bs):
     nq = 3
     ctx_lens = [3, bs + 2, 900, 2500]
@@ -79,7 +82,8 @@ def test_general_verify_matches_oracle(heads, kv, d, bs):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("heads,kv,d,bs", [(32, 8, 96, 32), (16, 2, 256, 8), (8, 8, 32, 1), (32, 8, 128, 32)])
+@pytest.mark.parametrize("heads,kv,d,bs", [(32, 8, 96, 32), (16, 2, 256, 8), (8, 8, 32, 1), (32, 8, 128, 32),
+                                         (64, 2, 96, 16)])
 def test_general_prefill_matches_oracle(dtype, heads, kv, d, bs):
     """Varlen causal chunks on cached prefixes, the chunks 1-200 tokens (more
     than one 64-position tile), a fresh prompt and a chunk on a long prefix."""
