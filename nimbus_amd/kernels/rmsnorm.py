@@ -20,36 +20,44 @@ MAX_COLS = 8192
 
 
 def _launch(x: torch.Tensor, residual: torch.Tensor | None, weight: torch.Tensor, eps: float):
+    # (An eager call of a small norm is bound by this function's host time, so
+    # it avoids reshapes, views and allocations that a 2-D input does not need.)
     n = x.shape[-1]
+    dt = x.dtype
     if weight.shape != (n,):
         raise ValueError(f"weight {tuple(weight.shape)} does not match rows of {n}")
-    if x.dtype not in (torch.float16, torch.bfloat16) or weight.dtype != x.dtype:
+    if (dt is not torch.float16 and dt is not torch.bfloat16) or weight.dtype != dt:
         raise NotImplementedError("fp16 or bf16 x and weight of one dtype")
-    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype):
+    if residual is not None and (residual.shape != x.shape or residual.dtype != dt):
         raise ValueError("residual must match x's shape and dtype")
     if not (x.is_cuda and weight.is_cuda and (residual is None or residual.is_cuda)):
         raise ValueError("rms_norm runs on the GPU only")
-    x2 = x.reshape(-1, n)
+    flat = x.dim() == 2
+    x2 = x if flat else x.reshape(-1, n)
     if x2.stride(-1) != 1:
         x2 = x2.contiguous()
-    weight = weight.contiguous()
-    out = torch.empty(x2.shape, dtype=x.dtype, device=x.device)
+    if weight.stride(0) != 1:
+        weight = weight.contiguous()
+    out = torch.empty_like(x2, memory_format=torch.contiguous_format)
     if residual is not None:
-        r2 = residual.reshape(-1, n)
+        r2 = residual if flat else residual.reshape(-1, n)
         if r2.stride(-1) != 1:
             r2 = r2.contiguous()
         res_out = torch.empty_like(out)
+        r_ptr, r_st, ro_ptr, ro_st = r2.data_ptr(), r2.stride(0), res_out.data_ptr(), res_out.stride(0)
     else:
-        r2 = res_out = None
+        res_out = None
+        r_ptr, r_st, ro_ptr, ro_st = None, 0, None, 0
     rows = x2.shape[0]
     if rows:
-        lib = _lib.load()
-        rc = lib.nimbus_add_rms_norm(
-            x2.data_ptr(), x2.stride(0), r2.data_ptr() if r2 is not None else None, r2.stride(0) if r2 is not None else 0,
-            weight.data_ptr(), out.data_ptr(), out.stride(0), res_out.data_ptr() if res_out is not None else None,
-            res_out.stride(0) if res_out is not None else 0, rows, n, float(eps), _lib.dtype_code(x.dtype),
+        rc = _lib.load().nimbus_add_rms_norm(
+            x2.data_ptr(), x2.stride(0), r_ptr, r_st, weight.data_ptr(), out.data_ptr(), out.stride(0), ro_ptr, ro_st,
+            rows, n, float(eps), _lib.NIMBUS_BFLOAT16 if dt is torch.bfloat16 else _lib.NIMBUS_FLOAT16,
             _lib.stream_of(x))
-        _lib.check(rc, "nimbus_add_rms_norm")
+        if rc:
+            _lib.check(rc, "nimbus_add_rms_norm")
+    if flat:
+        return out, res_out
     return out.view(x.shape), (res_out.view(x.shape) if res_out is not None else None)
 
 
