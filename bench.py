@@ -3,7 +3,8 @@
 
     python bench.py [--steps K] [--warmup W] [--all] [--no-cpu-baseline]
 
-Prints ONE JSON line. The headline is BASELINE config 3: Llama-3-8B-shaped
+Prints ONE JSON line. Configs 1-5 are nimbus_amd.workloads' five numbered
+configurations. The headline is config 3: Llama-3-8B-shaped
 paged decode attention (B=64, H=32, KV=8, D=128, bf16, contexts log-uniform
 in [128, 8192], K/V pages scattered over a pool 1.2x the pages needed).
 A step is one paged_decode_attention call on inputs already resident in HBM.
@@ -30,11 +31,11 @@ cpu_baseline the CPU oracle (restated nimbus/kernels/reference.py:71-96,
 reference_shapes the reference's own kernel micro-bench shapes
              (bench/kernels.py:54-74: TinyLlama heads, fp16) beside its
              published numbers (other hardware)
-prefill      BASELINE config 4's prefill part (4 chunks of 512 over cached
+prefill      config 4's prefill part (4 chunks of 512 over cached
              prefixes of up to 1024): causal FLOPs / mean time per call of K
              back-to-back calls, against the 2.5 PFLOP/s dense bf16 MFMA peak
-prefill_scaling the same prefill kernel on two larger workloads (not BASELINE
-             configs): one 8192-token prompt, and 64 chunks of 512 over
+prefill_scaling the same prefill kernel on two larger workloads (not among
+             configs 1-5): one 8192-token prompt, and 64 chunks of 512 over
              2048-token cached prefixes; at most 20 timed calls each
 mixed_step   the whole config-4 step: slot write of 2,108 tokens + prefill
              (eager) + the 60 decodes replayed from a hipGraph padded to 64;
@@ -56,7 +57,7 @@ int8_matmul  the INT8 weight-only matmul at Llama-3-8B decode projections
              (int8 weights, x, y, scales) / mean kernel time, against 8 TB/s,
              beside torch's dense matmul on the dequantized weights
 
-other_configs BASELINE configs 1, 2 and 5 in compact form (at most 50
+other_configs configs 1, 2 and 5 in compact form (at most 50
              timed calls each); they run before the headline, which is
              thereby measured with the GPU's clocks settled (config 3's calls
              run 2-7% slower over the first ~150 calls of a fresh process)
@@ -64,7 +65,7 @@ other_configs BASELINE configs 1, 2 and 5 in compact form (at most 50
 Between timed calls the K/V pool rotates over enough copies (>= 1.5 GB) that
 the 256 MB Infinity Cache cannot serve one call's pages to the next.
 
---all also times every BASELINE config (--all-out PATH writes the full rows as JSON).
+--all also times every config (1-5) (--all-out PATH writes the full rows as JSON).
 """
 
 from __future__ import annotations
@@ -92,7 +93,7 @@ def parse(argv=None):
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--all", action="store_true", help="also time every BASELINE config")
+    ap.add_argument("--all", action="store_true", help="also time every config (1-5)")
     ap.add_argument("--all-out", default=None, metavar="PATH", help="with --all: also write the full rows as JSON")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
@@ -361,7 +362,7 @@ def cpu_decode_baseline(batch, seconds):
 
 def cpu_prefill_baseline(batch, seconds):
     """The CPU oracle of paged prefill (nimbus/kernels/reference.py:37-68) on
-    CPU copies of BASELINE config 4's prefill part, in their dtype."""
+    CPU copies of config 4's prefill part, in their dtype."""
     import torch
 
     from nimbus_amd import workloads
@@ -389,7 +390,7 @@ def cpu_long_decode_baseline(batch, seconds):
     """The per-row form of the decode oracle (oracle/reference.py's
     decode_attention_rows: the math of nimbus/kernels/reference.py:71-96 one
     sequence at a time; the batched form would gather a [256, 32768, 8, 128]
-    tensor) on BASELINE config 5, row by row in batch order until `seconds`
+    tensor) on config 5, row by row in batch order until `seconds`
     of oracle time are spent: bytes of the rows done / their oracle time.
     Each row's pages are copied to the host before its timed call."""
     import torch
@@ -743,7 +744,7 @@ def time_int8_matmul(steps, warmup):
 
 def time_decode_step(steps, warmup, chain=16):
     """One decode step of a Llama-3-8B-shaped model (32 layers, random bf16
-    weights) for the 64 sequences of BASELINE config 3 (contexts
+    weights) for the 64 sequences of config 3 (contexts
     log-uniform [128, 8192]), through DecodeGraphs: eager, one graph replay
     per step, and greedy_chain (step graph + on-device token pick, no host
     round trip); then the same with the decoder projections quantized to
@@ -820,7 +821,7 @@ def time_decode_step(steps, warmup, chain=16):
                 "verify_pass_ms": verify_ms, "verify_query_tokens": 64 * 5,
                 "verify_query_tokens_per_s": 64 * 5 / (verify_ms * 1e-3)}
 
-    res = {"workload": "Llama-3-8B shape (random weights), 64 decode sequences of BASELINE config 3 "
+    res = {"workload": "Llama-3-8B shape (random weights), 64 decode sequences of config 3 "
                        f"(sum ctx {sum(ctx)}), chains of {chain} greedy steps",
            "runs": [measure("bf16")]}
     quantize_model(model)
@@ -940,7 +941,7 @@ def reference_shapes(reps=200, warmup=25):
 # ---------------------------------------------------------------- configs 1, 2 and 5
 
 def other_configs(steps, warmup, prefill=True):
-    """BASELINE configs 1 (TinyLlama decode), 2 (TinyLlama varlen prefill)
+    """configs 1 (TinyLlama decode), 2 (TinyLlama varlen prefill)
     and 5 (long-context decode, ~40 GB pool) in compact form: µs per call of
     back-to-back calls (decode: also replayed from a hipGraph, which drops the
     ~15 µs of host work per eager call that bounds config 1), GB/s or TFLOP/s
@@ -1016,7 +1017,7 @@ def all_configs(steps, warmup, out_path=None):
 # ---------------------------------------------------------------- main
 
 def config_summary(result):
-    """One compact entry per BASELINE config: µs per call and the roofline
+    """One compact entry per config: µs per call and the roofline
     fraction (HBM for decode, dense MFMA for prefill)."""
     def r4(x):
         return None if x is None else round(float(x), 4)
@@ -1100,7 +1101,7 @@ def main(argv=None):
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q, 0.5*N(0,1) K/V, shuffled page tables)",
         "config": {
-            "workload": "llama3_decode: BASELINE config 3, Llama-3-8B-shaped paged decode attention",
+            "workload": "llama3_decode: config 3, Llama-3-8B-shaped paged decode attention",
             "batch": dec["batch"], "heads": 32, "kv_heads": 8, "head_dim": 128, "block_size": 16,
             "context": "log-uniform [128, 8192], seed 0", "sum_ctx": dec["sum_ctx"],
             "bytes_per_call": dec["bytes"], "pool_rotation": dec["pools"], "parallelism": "none (1 GPU)",
@@ -1176,7 +1177,7 @@ def main(argv=None):
             torch.cuda.empty_cache()
         result["cpu_baseline"] = dict(base, entries=entries)
     # Last on the line (and repeated on stderr after it), where a reader of the output's tail finds it: one
-    # figure per BASELINE config and its share of the roofline.
+    # figure per config and its share of the roofline.
     result["summary"] = summary = config_summary(result)
     print(json.dumps(result), flush=True)
     for k, v in summary.items():

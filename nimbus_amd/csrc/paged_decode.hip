@@ -64,7 +64,7 @@ namespace nimbus {
 constexpr int kPage = 16;             // tokens per page (the only block size)
 // Slices shorter than this only add merge work. Big batches never reach it
 // (their slices are bounded by the resident waves); a short batch takes
-// more, shorter slices: BASELINE config 1 (16 sequences, 530 pages per kv
+// more, shorter slices: config 1 (16 sequences, 530 pages per kv
 // head) measured 14.8 us per call at 8 pages, 12.7 at 4, 11.9 at 2, with
 // configs 3 and 5 unchanged.
 constexpr int kMinPagesPerWave = 2;

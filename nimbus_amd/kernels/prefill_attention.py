@@ -78,7 +78,7 @@ def build_programs(query_start_host: list[int], device,
     apart, which share a CU, pair a heavy tile with a light one. A table of
     up to LPT_TILES tiles, whose last workgroups wait for a free slot, goes
     strictly heaviest tile first (measured 6% faster than sequence order on
-    BASELINE config 2's 36 tiles), so the late starters are the light ones.
+    config 2's 36 tiles), so the late starters are the light ones.
     """
     qs = np.asarray(query_start_host, dtype=np.int64)
     lens = np.diff(qs) if qs.size > 1 else np.zeros(0, dtype=np.int64)

@@ -7,18 +7,20 @@ table[p // 16] * 16 + p % 16 (runner.py:61); tables are zero-padded to the
 widest row (runner.py:24-30); a flat batch is ordered prefill-first.
 
 The five named configurations are the ones the benchmark and the parity tests
-use (values N(0,1) unless stated, scale 1/sqrt(D)):
+use, numbered 1-5 as comments elsewhere refer to them ("config 3"), values
+N(0,1) unless stated, scale 1/sqrt(D):
 
-  tinyllama_decode     B=16, H=32, KV=4, D=64, fp16, ctx U[16,1024], tables
-                       consecutive slices of a permutation of a 1,100 pool
-  tinyllama_prefill    8 seqs, new q_len U[32,512] on prefix U[0,256],
-                       H=32, KV=4, D=64, fp16
-  llama3_decode        B=64, H=32, KV=8, D=128, bf16, ctx log-U[128,8192],
-                       K/V 0.5*N(0,1), pool 1.2x the pages needed
-  llama3_mixed         4 prefill chunks of 512 on prefix U[0,1024], then 60
-                       decodes with ctx U[256,4096], bf16
-  llama3_long_decode   B=256, 90% ctx U[512,4096], 10% U[16384,32768], pool
-                       of ~40 GB K+V, tables random pages from it
+  1 tinyllama_decode     B=16, H=32, KV=4, D=64, fp16, ctx U[16,1024], tables
+                         consecutive slices of a permutation of a 1,100 pool
+  2 tinyllama_prefill    8 seqs, new q_len U[32,512] on prefix U[0,256],
+                         H=32, KV=4, D=64, fp16
+  3 llama3_decode        B=64, H=32, KV=8, D=128, bf16, ctx log-U[128,8192],
+                         K/V 0.5*N(0,1), pool 1.2x the pages needed (the
+                         benchmark's headline)
+  4 llama3_mixed         4 prefill chunks of 512 on prefix U[0,1024], then 60
+                         decodes with ctx U[256,4096], bf16
+  5 llama3_long_decode   B=256, 90% ctx U[512,4096], 10% U[16384,32768], pool
+                         of ~40 GB K+V, tables random pages from it
 """
 
 from __future__ import annotations

@@ -11,7 +11,7 @@ Each function follows one function of the reference, op for op:
   paged_decode_attention  nimbus/kernels/reference.py:71-96
   decode_attention_rows   same mathematics as :71-96, one sequence at a time,
                           for batches whose padded gather does not fit in host
-                          memory (~34 GB batched)
+                          memory (config 5: ~34 GB batched)
   rms_norm                nimbus/kernels/reference.py:99-104
   add_rms_norm            nimbus/kernels/reference.py:107-112
   quantize_weight         nimbus/quant/int8.py:20-25

@@ -28,7 +28,7 @@ def _meta(b: workloads.PagedBatch) -> AttnMetadata:
 
 
 def test_mixed_step_matches_oracle():
-    """BASELINE config 4 layout: 4 prefill chunks of 512 over cached prefixes,
+    """config 4 layout: 4 prefill chunks of 512 over cached prefixes,
     then 60 decodes, flat and prefill-first; the backend writes the new K/V
     first (write_first=False here so the backend's own write is what counts)."""
     announce("backend mixed step (llama3_mixed)")
@@ -52,7 +52,7 @@ def test_mixed_step_matches_oracle():
 
 
 def test_config4_step_with_graph_replayed_decode():
-    """BASELINE config 4 as the bench runs it: the slot write of the prefill
+    """config 4 as the bench runs it: the slot write of the prefill
     tokens and the prefill (eager), then the 60 decodes (contexts U[256,
     4096]) replayed from DecodeAttentionGraphs padded to 64, whose graph
     writes the decode tokens' K/V itself. Both parts against the oracle, the

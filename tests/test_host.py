@@ -372,7 +372,7 @@ def _stream_case(lens, prefix):
 
 
 @pytest.mark.parametrize("lens,prefix,heads,kv", [
-    ([512] * 4, [831, 87, 183, 242], 32, 8),   # BASELINE config 4's prefill part (its seed's prefixes)
+    ([512] * 4, [831, 87, 183, 242], 32, 8),   # config 4's prefill part (its seed's prefixes)
     ([300, 17, 64, 0, 1, 900], [0, 5000, 64, 12, 0, 33], 32, 8),
     ([8192], [0], 32, 8),                       # one long prompt: many units per share
     ([130, 64, 40], [4000, 8000, 300], 32, 8),  # few heavy units: units cut across many shares

@@ -39,7 +39,7 @@ def _with_workspace(q, kc, vc, ctx, bt, maxc, scale):
 
 
 def test_noalloc_matches_workspace_entry_point_twice():
-    # Call 1: BASELINE config 3 (B=64, Llama-3-8B heads, bf16, contexts up to 8192).
+    # Call 1: config 3 (B=64, Llama-3-8B heads, bf16, contexts up to 8192).
     announce("noalloc call 1: llama3_decode (config 3)")
     big = workloads.llama3_decode("cuda")
     a = big.decode_args()
