@@ -99,6 +99,18 @@ def test_prefix_in_registers_and_in_lds(batch):
     assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale), what="vs oracle")
 
 
+def test_largest_batch():
+    """4096 sequences, the most the page prefix in LDS holds (4097 is refused
+    before launch, tests/test_capi.py): short contexts of 1-40 tokens, so most
+    slices hold several whole sequences, against the batched oracle."""
+    announce("decode B=4096 (largest batch)")
+    g = torch.Generator().manual_seed(4096)
+    ctx_lens = [int(c) for c in torch.randint(1, 41, (4096,), generator=g)]
+    q, k, v, ctx, bt, scale = _case(32, 8, 128, ctx_lens, torch.bfloat16, seed=4096)
+    got = paged_decode_attention(q, k, v, ctx, bt, max(ctx_lens), scale)
+    assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale, batched=True), what="vs oracle")
+
+
 def test_grid_width_does_not_change_results():
     """A wider grid (larger max_context, as under graph capture) only adds
     partitions that exit at once: results are bit-identical."""
