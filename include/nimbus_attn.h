@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 13
+#define NIMBUS_ATTN_ABI_VERSION 14
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -347,7 +347,7 @@ int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const void* w_pac
 /*
  * nimbus_int8_matmul_packed with an explicit launch plan, for a caller that
  * tunes per shape (as the reference's triton.autotune does per M bucket,
- * N and K): bm tokens per workgroup tile (16, 32 or 64), ks k slices per
+ * N and K): bm tokens per workgroup tile (16, 32, 64 or 128), ks k slices per
  * workgroup (1, 2, 4 or 8, with ks * bm <= 128), splits of K (1..16) and
  * rows_per_wave 16-row blocks per wave (1 or 2). Any valid plan gives y to
  * fp32 summation order; the workspace is
@@ -362,6 +362,23 @@ int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* 
                                    int64_t y_stride, int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
                                    int32_t splits, int32_t rows_per_wave, void* workspace, int64_t workspace_bytes,
                                    int32_t dtype, void* stream);
+
+/*
+ * The MLP's gate_up projection and SiLU gate in one launch. Replaces
+ * MLP.forward's F.silu(gate) * up over Int8Linear's output
+ * (nimbus/model/llama.py:100-103, nimbus/quant/int8.py:43-47): w_packed holds
+ * gate_up_proj's n = 2 * intermediate rows (gate rows first), and y [m, n/2]
+ * receives what nimbus_silu_mul would make of nimbus_int8_matmul_packed's
+ * [m, n] output, bit for bit, without that output being written. n a multiple
+ * of 32, k of 8; one split of K: bm (16, 32, 64 or 128; 0 picks from m with
+ * ks = 1 and one row block per wave), ks (1, 2 or 4, ks * bm <= 128) and
+ * rows_per_wave (1 or 2) as for nimbus_int8_matmul_packed_plan. The tiled
+ * kernel's alignment and size rules apply (an error otherwise, no other
+ * path); y must not overlap x. No workspace.
+ */
+int nimbus_int8_matmul_packed_silu(const void* x, int64_t x_stride, const void* w_packed, const void* scale, void* y,
+                                   int64_t y_stride, int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
+                                   int32_t rows_per_wave, int32_t dtype, void* stream);
 
 /*
  * Rotary position embedding, in place. Replaces Rotary.forward

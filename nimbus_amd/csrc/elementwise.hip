@@ -27,6 +27,7 @@
 // cache slot advance.
 #include "common.h"
 #include "nimbus_attn_internal.h"
+#include "silu.h"
 
 namespace nimbus {
 
@@ -181,8 +182,7 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(SiluArgs a) {
     for (int b = 0; b < 2; ++b) {
       const float gv = Elem<DT>::to_f32(static_cast<uint16_t>(g[e] >> (16 * b)));
       const float uv = Elem<DT>::to_f32(static_cast<uint16_t>(u[e] >> (16 * b)));
-      const float s = rnd<DT>(gv / (1.f + expf(-gv)));
-      v[b] = Elem<DT>::from_f32(s * uv);
+      v[b] = silu_mul_value<DT>(gv, uv);
     }
     o[e] = pack2(v[0], v[1]);
   }

@@ -29,6 +29,7 @@
 
 #include "common.h"
 #include "nimbus_attn_internal.h"
+#include "silu.h"
 
 namespace nimbus {
 
@@ -76,6 +77,22 @@ __device__ __forceinline__ int x_chunk(int t, int c) {
 __device__ __forceinline__ int x_chunk_at(int t, int p) {
   const int u = p ^ (t & 7);
   return ((u << 1) & 6) | (u >> 2);
+}
+
+// dtype(acc * scale) as the reference forms it: the fp32 product, then the
+// conversion to the 16-bit type. Left to itself the compiler turns some of
+// these into one v_fma_mixlo_f16 (the exact product rounded to 16 bits once)
+// and others into a multiply and a conversion, picking per element and per
+// kernel: about one output in 10^4 then differs by an ulp between two
+// kernels that store the same value (measured on the fused gate_up + SiLU
+// launch against the projection and the gate run apart). The empty asm keeps
+// the fp32 product in a register, so every store rounds twice, as the
+// reference does.
+template <int DT>
+__device__ __forceinline__ uint16_t scaled(float acc, float scale) {
+  float p = acc * scale;
+  asm volatile("" : "+v"(p));
+  return Elem<DT>::from_f32(p);
 }
 
 // Eight int8 (two dwords) -> the eight fp16 / bf16 of an MFMA operand.
@@ -264,8 +281,8 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_kernel(GemmArgs a) {
       const int m = m0 + 16 * cb + col;
       if (m < a.M) {
         const f32x4 o = acc[cb];
-        const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(o[0] * sc[0]), Elem<DT>::from_f32(o[1] * sc[1])),
-                              pack2(Elem<DT>::from_f32(o[2] * sc[2]), Elem<DT>::from_f32(o[3] * sc[3]))};
+        const u32x2 v = u32x2{pack2(scaled<DT>(o[0], sc[0]), scaled<DT>(o[1], sc[1])),
+                              pack2(scaled<DT>(o[2], sc[2]), scaled<DT>(o[3], sc[3]))};
         *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
       }
     }
@@ -297,8 +314,8 @@ __global__ __launch_bounds__(256) void int8_matmul_reduce_kernel(GemmArgs a) {
   const u32x2 sw = *reinterpret_cast<const u32x2*>(a.scale + n);
   const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
                        Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
-  const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(s[0] * sc[0]), Elem<DT>::from_f32(s[1] * sc[1])),
-                        pack2(Elem<DT>::from_f32(s[2] * sc[2]), Elem<DT>::from_f32(s[3] * sc[3]))};
+  const u32x2 v = u32x2{pack2(scaled<DT>(s[0], sc[0]), scaled<DT>(s[1], sc[1])),
+                        pack2(scaled<DT>(s[2], sc[2]), scaled<DT>(s[3], sc[3]))};
   *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
 }
 
@@ -373,7 +390,12 @@ struct PackShape {
 };
 
 // Grid: (ceil(N / 16 / (RB RW)) row tiles, splits, M / BM token tiles).
-template <int DT, int BM, int KS, int RW>
+// SILU: the projection is Llama's gate_up (gate rows [0, N/2), up rows
+// [N/2, N)) and y = silu(gate) * up, [M, N/2]: the first RB/2 row-block groups
+// of a workgroup take gate rows and the others the matching up rows, so that
+// after the k-slice sum each up wave hands its rounded outputs to its gate
+// partner through LDS (one split only; grid x = ceil(N / 32 / (RB/2 RW))).
+template <int DT, int BM, int KS, int RW, bool SILU>
 __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmArgs a) {
   constexpr int CB = BM / 16;
   constexpr int RB = PackShape<BM, KS, RW>::RB;
@@ -398,7 +420,12 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
   const int rb = wave / KS;
   const int nblocks = (a.N + 15) / 16;
   const int kchunks = (a.K + 63) / 64;
-  const int nb0 = (blockIdx.x * RB + rb) * RW;
+  constexpr int HRB = RB / 2;
+  static_assert(!SILU || RB % 2 == 0, "gate and up row blocks pair up");
+  const int hb = a.N / 32;  // gate row blocks (SILU)
+  int nb0;
+  if constexpr (SILU) nb0 = rb < HRB ? (blockIdx.x * HRB + rb) * RW : hb + (blockIdx.x * HRB + rb - HRB) * RW;
+  else nb0 = (blockIdx.x * RB + rb) * RW;
   const int c0 = blockIdx.y * (a.ksplit / 64);
   const int ce = min(kchunks, c0 + a.ksplit / 64);
   const int m0 = blockIdx.z * BM;
@@ -546,14 +573,70 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
         for (int cb = 0; cb < CB; ++cb) red[((((ks - 1) * RB + rb) * RW + j) * CB + cb) * 64 + lane] = acc[j][cb];
     }
     lds_barrier();
-    if (ks > 0) return;
-#pragma unroll
-    for (int t = 1; t < KS; ++t) {
-#pragma unroll
-      for (int j = 0; j < RW; ++j)
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) acc[j][cb] += red[((((t - 1) * RB + rb) * RW + j) * CB + cb) * 64 + lane];
+    if constexpr (!SILU) {
+      if (ks > 0) return;
     }
+    if (ks == 0) {
+#pragma unroll
+      for (int t = 1; t < KS; ++t) {
+#pragma unroll
+        for (int j = 0; j < RW; ++j)
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) acc[j][cb] += red[((((t - 1) * RB + rb) * RW + j) * CB + cb) * 64 + lane];
+      }
+    }
+  }
+
+  if constexpr (SILU) {
+    // Every wave reaches both barriers (none has returned); the first also
+    // ends the x reads (one k slice) or the k-slice sums' reads of LDS.
+    lds_barrier();
+    u32x2* ex = reinterpret_cast<u32x2*>(xs);  // [RB/2][RW][CB][64 lanes]: the up rows' outputs
+    if (ks == 0 && rb >= HRB) {
+#pragma unroll
+      for (int j = 0; j < RW; ++j) {
+        const int n = 16 * (nb0 + j) + 4 * grp;
+        u32x2 sw = u32x2{0u, 0u};
+        if (n < a.N) sw = *reinterpret_cast<const u32x2*>(a.scale + n);
+        const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
+                             Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const f32x4 o = acc[j][cb];
+          ex[(((rb - HRB) * RW + j) * CB + cb) * 64 + lane] =
+              u32x2{pack2(scaled<DT>(o[0], sc[0]), scaled<DT>(o[1], sc[1])),
+                    pack2(scaled<DT>(o[2], sc[2]), scaled<DT>(o[3], sc[3]))};
+        }
+      }
+    }
+    lds_barrier();
+    if (ks == 0 && rb < HRB) {
+#pragma unroll
+      for (int j = 0; j < RW; ++j) {
+        if (nb0 + j >= hb) continue;  // past the gate half: the tile's last groups
+        const int n = 16 * (nb0 + j) + 4 * grp;
+        const u32x2 sw = *reinterpret_cast<const u32x2*>(a.scale + n);
+        const float sc[4] = {Elem<DT>::to_f32(static_cast<uint16_t>(sw[0])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[0] >> 16)),
+                             Elem<DT>::to_f32(static_cast<uint16_t>(sw[1])), Elem<DT>::to_f32(static_cast<uint16_t>(sw[1] >> 16))};
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const int m = m0 + 16 * cb + col;
+          if (m < a.M) {
+            const f32x4 o = acc[j][cb];
+            const u32x2 up = ex[((rb * RW + j) * CB + cb) * 64 + lane];
+            uint16_t v[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float g = Elem<DT>::to_f32(scaled<DT>(o[e], sc[e]));
+              const float u = Elem<DT>::to_f32(static_cast<uint16_t>(up[e / 2] >> (16 * (e % 2))));
+              v[e] = silu_mul_value<DT>(g, u);
+            }
+            *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = u32x2{pack2(v[0], v[1]), pack2(v[2], v[3])};
+          }
+        }
+      }
+    }
+    return;
   }
 
 #pragma unroll
@@ -569,8 +652,8 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
         const int m = m0 + 16 * cb + col;
         if (m < a.M) {
           const f32x4 o = acc[j][cb];
-          const u32x2 v = u32x2{pack2(Elem<DT>::from_f32(o[0] * sc[0]), Elem<DT>::from_f32(o[1] * sc[1])),
-                                pack2(Elem<DT>::from_f32(o[2] * sc[2]), Elem<DT>::from_f32(o[3] * sc[3]))};
+          const u32x2 v = u32x2{pack2(scaled<DT>(o[0], sc[0]), scaled<DT>(o[1], sc[1])),
+                                pack2(scaled<DT>(o[2], sc[2]), scaled<DT>(o[3], sc[3]))};
           *reinterpret_cast<u32x2*>(a.y + static_cast<int64_t>(m) * a.sy + n) = v;
         }
       }
@@ -658,11 +741,21 @@ static PackPlan packed_plan(int64_t m, int32_t n, int32_t k) {
   return p;
 }
 
-template <int DT, int BM, int KS, int RW>
+template <int DT, int BM, int KS, int RW, bool SILU>
 static int launch_packed(const GemmArgs& a, hipStream_t s) {
   constexpr int RB = PackShape<BM, KS, RW>::RB;
+  if constexpr (SILU) {
+    if constexpr (RB % 2 != 0) {
+      return NIMBUS_ERR_UNSUPPORTED;
+    } else {
+      const int hrw = RB / 2 * RW;
+      const dim3 grid((a.N / 32 + hrw - 1) / hrw, 1, (a.M + BM - 1) / BM);
+      hipLaunchKernelGGL((int8_matmul_packed_kernel<DT, BM, KS, RW, true>), grid, dim3(kGemmThreads), 0, s, a);
+      return static_cast<int>(hipGetLastError());
+    }
+  }
   const dim3 grid(((a.N + 15) / 16 + RB * RW - 1) / (RB * RW), a.splits, (a.M + BM - 1) / BM);
-  hipLaunchKernelGGL((int8_matmul_packed_kernel<DT, BM, KS, RW>), grid, dim3(kGemmThreads), 0, s, a);
+  hipLaunchKernelGGL((int8_matmul_packed_kernel<DT, BM, KS, RW, false>), grid, dim3(kGemmThreads), 0, s, a);
   if (a.splits > 1) {
     const int64_t quads = static_cast<int64_t>(a.M) * (a.N / 4);
     hipLaunchKernelGGL((int8_matmul_reduce_kernel<DT>), dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256),
@@ -671,28 +764,30 @@ static int launch_packed(const GemmArgs& a, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <int DT, int BM, int KS>
+template <int DT, int BM, int KS, bool SILU>
 static int launch_packed_rw(const GemmArgs& a, int rw, hipStream_t s) {
-  return rw == 2 ? launch_packed<DT, BM, KS, 2>(a, s) : launch_packed<DT, BM, KS, 1>(a, s);
+  return rw == 2 ? launch_packed<DT, BM, KS, 2, SILU>(a, s) : launch_packed<DT, BM, KS, 1, SILU>(a, s);
 }
 
-template <int DT, int BM>
+template <int DT, int BM, bool SILU>
 static int launch_packed_bm(const GemmArgs& a, int ks, int rw, hipStream_t s) {
   switch (ks) {
-    case 1: return launch_packed_rw<DT, BM, 1>(a, rw, s);
-    case 2: if constexpr (BM <= 64) return launch_packed_rw<DT, BM, 2>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
-    case 4: if constexpr (BM <= 32) return launch_packed_rw<DT, BM, 4>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
-    default: if constexpr (BM <= 16) return launch_packed_rw<DT, BM, 8>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
+    case 1: return launch_packed_rw<DT, BM, 1, SILU>(a, rw, s);
+    case 2: if constexpr (BM <= 64) return launch_packed_rw<DT, BM, 2, SILU>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
+    case 4: if constexpr (BM <= 32) return launch_packed_rw<DT, BM, 4, SILU>(a, rw, s); else return NIMBUS_ERR_UNSUPPORTED;
+    default:
+      if constexpr (BM <= 16 && !SILU) return launch_packed_rw<DT, BM, 8, SILU>(a, rw, s);
+      else return NIMBUS_ERR_UNSUPPORTED;
   }
 }
 
-template <int DT>
+template <int DT, bool SILU = false>
 static int launch_packed_dt(const GemmArgs& a, const PackPlan& p, hipStream_t s) {
   switch (p.bm) {
-    case 16: return launch_packed_bm<DT, 16>(a, p.ks, p.rw, s);
-    case 32: return launch_packed_bm<DT, 32>(a, p.ks, p.rw, s);
-    case 128: return launch_packed_bm<DT, 128>(a, p.ks, p.rw, s);
-    default: return launch_packed_bm<DT, 64>(a, p.ks, p.rw, s);
+    case 16: return launch_packed_bm<DT, 16, SILU>(a, p.ks, p.rw, s);
+    case 32: return launch_packed_bm<DT, 32, SILU>(a, p.ks, p.rw, s);
+    case 128: return launch_packed_bm<DT, 128, SILU>(a, p.ks, p.rw, s);
+    default: return launch_packed_bm<DT, 64, SILU>(a, p.ks, p.rw, s);
   }
 }
 
@@ -739,7 +834,7 @@ __global__ __launch_bounds__(kGeneralThreads) void int8_matmul_general_kernel(Ge
     float acc = 0.f;
     for (int k = 0; k < a.K; ++k)
       acc = __builtin_fmaf(Elem<DT>::to_f32(xr[k]), static_cast<float>(general_weight<PACKED>(a, n, k)), acc);
-    a.y[m * a.sy + n] = Elem<DT>::from_f32(acc * sc);
+    a.y[m * a.sy + n] = scaled<DT>(acc, sc);
   }
 }
 
@@ -957,4 +1052,57 @@ extern "C" int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, c
   if (!make_plan(m, n, k, bm, ks, splits, rows_per_wave, &p)) return NIMBUS_ERR_UNSUPPORTED;
   return packed_impl(x, x_stride, w_packed, scale, y, y_stride, m, n, k, &p, workspace, workspace_bytes, dtype,
                      stream);
+}
+
+// Llama's gate_up projection fused with its SiLU gate: y [m, n/2] =
+// silu(gate) * up of the projection's outputs gate = [:, :n/2], up =
+// [:, n/2:] (each rounded to the model dtype first, as the projection would
+// store them), without writing the projection's output. A plan of one split
+// (bm, ks in 1, 2, 4, rows_per_wave); bm = 0 takes bm from m, one k slice,
+// one row block per wave.
+extern "C" int nimbus_int8_matmul_packed_silu(const void* x, int64_t x_stride, const void* w_packed,
+                                              const void* scale, void* y, int64_t y_stride, int64_t m, int32_t n,
+                                              int32_t k, int32_t bm, int32_t ks, int32_t rows_per_wave,
+                                              int32_t dtype, void* stream) {
+  if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (n % 32 != 0 || !packed_shape_ok(n, k)) return NIMBUS_ERR_UNSUPPORTED;
+  if (bm == 0) {
+    bm = gemm_bm(m);
+    ks = 1;
+    rows_per_wave = 1;
+  }
+  PackPlan p;
+  if (ks == 8 || !make_plan(m, n, k, bm, ks, 1, rows_per_wave, &p) || p.splits != 1) return NIMBUS_ERR_UNSUPPORTED;
+  if (m == 0) return NIMBUS_OK;
+  if (!x || !w_packed || !scale || !y) return NIMBUS_ERR_INVALID;
+  if (x_stride < k || y_stride < n / 2) return NIMBUS_ERR_INVALID;
+  if (!elements_aligned(x, scale, y)) return NIMBUS_ERR_ALIGNMENT;
+  const int64_t x_bytes = ((m - 1) * x_stride + k) * 2;
+  const int64_t w_bytes = packed_bytes(n, k);
+  if (m > (int64_t{1} << 21) || x_bytes >= (int64_t{1} << 31) || w_bytes >= (int64_t{1} << 31))
+    return NIMBUS_ERR_UNSUPPORTED;
+  if (x_stride % 8 != 0 || y_stride % 4 != 0 ||
+      (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed) | reinterpret_cast<uintptr_t>(y)) %
+              16 != 0 ||
+      reinterpret_cast<uintptr_t>(scale) % 8 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
+  GemmArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.sx = static_cast<int32_t>(x_stride);
+  a.w = static_cast<const int8_t*>(w_packed);
+  a.sw = 0;
+  a.x_bytes = static_cast<int32_t>(x_bytes);
+  a.w_bytes = static_cast<int32_t>(w_bytes);
+  a.scale = static_cast<const uint16_t*>(scale);
+  a.y = static_cast<uint16_t*>(y);
+  a.sy = y_stride;
+  a.part = nullptr;
+  a.M = static_cast<int32_t>(m);
+  a.N = n;
+  a.K = k;
+  a.splits = 1;
+  a.ksplit = p.ksplit;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == kFloat16 ? launch_packed_dt<kFloat16, true>(a, p, s) : launch_packed_dt<kBFloat16, true>(a, p, s);
 }

@@ -239,3 +239,88 @@ def int8_matmul_packed(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Ten
             *plan, ws_ptr, ws_bytes, _lib.dtype_code(x.dtype), _lib.stream_of(x))
     _lib.check(rc, "nimbus_int8_matmul_packed")
     return y.view(*shape[:-1], n) if out is None else y
+
+
+def _silu_plans(m: int, n: int, k: int) -> list[tuple[int, int, int]]:
+    """Candidate plans (bm, ks, rows per wave) of the fused gate_up + SiLU
+    launch: the single-split plans whose row-block groups pair up (ks <= 4)."""
+    return sorted({(bm, ks, rw) for bm, ks, splits, rw in _candidate_plans(m, n, k) if splits == 1 and ks <= 4})
+
+
+_SILU_TUNED: dict[tuple, tuple[int, int, int] | None] = {}
+
+
+def _tune_silu(x2, w_packed, scale, y, n, k, lib) -> tuple[int, int, int] | None:
+    m = x2.shape[0]
+    plans = _silu_plans(m, n, k)
+    if len(plans) < 2:
+        return plans[0] if plans else None
+    copies = [w_packed] + [w_packed.clone() for _ in range(max(0, int(_TUNE_BYTES // w_packed.numel()) - 1))]
+    stream = torch.cuda.current_stream(x2.device)
+    dt = _lib.dtype_code(x2.dtype)
+
+    def run(plan, w):
+        rc = lib.nimbus_int8_matmul_packed_silu(x2.data_ptr(), x2.stride(0), w.data_ptr(), scale.data_ptr(),
+                                                y.data_ptr(), y.stride(0), m, n, k, *plan, dt, stream.cuda_stream)
+        _lib.check(rc, "nimbus_int8_matmul_packed_silu")
+
+    best, best_t = None, float("inf")
+    for plan in plans:
+        run(plan, copies[0])
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for rep in range(2):
+            for w in copies:
+                run(plan, w)
+        end.record(stream)
+        end.synchronize()
+        t = start.elapsed_time(end)
+        if t < best_t:
+            best, best_t = plan, t
+    return best
+
+
+def int8_matmul_packed_silu(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor, n: int, k: int,
+                            out: torch.Tensor | None = None) -> torch.Tensor:
+    """silu_mul(int8_matmul_packed(x, w_packed, scale, n, k)) in one launch,
+    bit for bit (the MLP's gate_up projection and SiLU gate,
+    nimbus/model/llama.py:100-103): [..., n / 2]. n a multiple of 32 (gate
+    rows first, then up rows); the plan is tuned per shape as
+    int8_matmul_packed's is."""
+    if w_packed.dtype != torch.int8 or w_packed.shape != (-(-n // 16), -(-k // 64), 1024):
+        raise ValueError("w_packed must be pack_int8_weight's layout for [n, k]")
+    if n % 32 != 0:
+        raise NotImplementedError("the fused gate needs n a multiple of 32")
+    if x.shape[-1] != k:
+        raise ValueError(f"x [..., {x.shape[-1]}] does not match k {k}")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise NotImplementedError("fp16 or bf16 activations")
+    if scale.shape != (n,) or scale.dtype != x.dtype:
+        raise ValueError(f"scale must be [{n}] in x's dtype")
+    if not (x.is_cuda and w_packed.is_cuda and scale.is_cuda):
+        raise ValueError("int8_matmul_packed_silu runs on the GPU only")
+    shape = x.shape
+    x2 = x.reshape(-1, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    m = x2.shape[0]
+    h = n // 2
+    if out is None:
+        y = torch.empty((m, h), dtype=x.dtype, device=x.device)
+    else:
+        if out.shape != (m, h) or out.dtype != x.dtype or out.stride(-1) != 1:
+            raise ValueError(f"out must be [{m}, {h}] in x's dtype with unit last stride")
+        y = out
+    if m == 0:
+        return y.view(*shape[:-1], h)
+    lib = _lib.load()
+    scale = scale.contiguous()
+    key = (m_bucket(m), n, k, x.dtype, x.device.index)
+    if key not in _SILU_TUNED and AUTOTUNE and not torch.cuda.is_current_stream_capturing():
+        _SILU_TUNED[key] = _tune_silu(x2, w_packed, scale, y, n, k, lib)
+    plan = _SILU_TUNED.get(key) or (0, 1, 1)
+    rc = lib.nimbus_int8_matmul_packed_silu(x2.data_ptr(), x2.stride(0), w_packed.data_ptr(), scale.data_ptr(),
+                                            y.data_ptr(), y.stride(0), m, n, k, *plan, _lib.dtype_code(x.dtype),
+                                            _lib.stream_of(x))
+    _lib.check(rc, "nimbus_int8_matmul_packed_silu")
+    return y.view(*shape[:-1], h) if out is None else y

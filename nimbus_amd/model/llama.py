@@ -127,7 +127,13 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(self.inter, cfg.hidden_size, bias=False)
 
     def forward(self, x):
-        return self.down_proj(silu_mul(self.gate_up_proj(x)))
+        # An INT8 gate_up projection runs with the SiLU gate in its epilogue
+        # (the same bits as the two steps, one launch and no [M, 2I] output).
+        fused = getattr(self.gate_up_proj, "forward_silu", None)
+        h = fused(x) if fused is not None else None
+        if h is None:
+            h = silu_mul(self.gate_up_proj(x))
+        return self.down_proj(h)
 
 
 class DecoderLayer(nn.Module):

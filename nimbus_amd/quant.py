@@ -13,7 +13,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from nimbus_amd.kernels.int8_matmul import int8_matmul_packed, pack_int8_weight, unpack_int8_weight
+from nimbus_amd.kernels.int8_matmul import (int8_matmul_packed, int8_matmul_packed_silu, pack_int8_weight,
+                                             unpack_int8_weight)
 
 
 def quantize_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -56,6 +57,14 @@ class Int8Linear(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return int8_matmul_packed(x, self.weight_packed, self.scale, self.out_features, self.in_features)
+
+    def forward_silu(self, x: torch.Tensor) -> torch.Tensor | None:
+        """silu_mul(self(x)) in one launch, bit for bit, for the MLP's gate_up
+        projection (gate rows first); None when out_features is not a
+        multiple of 32 (the caller then runs the two steps)."""
+        if self.out_features % 32 != 0:
+            return None
+        return int8_matmul_packed_silu(x, self.weight_packed, self.scale, self.out_features, self.in_features)
 
 
 # Attribute names of the decoder's projections (nimbus/model/llama.py): the

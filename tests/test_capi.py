@@ -222,6 +222,30 @@ def test_int8_matmul_rejects_before_launch():
     assert ws(-1, 4, 16) == -1
 
 
+def test_int8_packed_silu_rejects_before_launch():
+    """The fused gate_up + SiLU entry refuses shapes, plans, null pointers,
+    short strides and misalignment with an error code, before any launch."""
+    lib = _lib.load()
+    f = lib.nimbus_int8_matmul_packed_silu
+    args = lambda m, n, k, **kw: dict(x=DUMMY, xs=k, w=DUMMY, s=DUMMY, y=DUMMY, ys=n // 2, m=m, n=n, k=k, bm=0,
+                                      ks=1, rw=1, dt=1, stream=None) | kw
+    call = lambda **kw: f(*kw.values())
+    assert call(**args(-1, 28672, 4096)) == _lib.NIMBUS_ERR_INVALID
+    assert call(**args(4, 4112, 4096)) == _lib.NIMBUS_ERR_UNSUPPORTED  # n not a multiple of 32
+    assert call(**args(4, 28672, 4092)) == _lib.NIMBUS_ERR_UNSUPPORTED  # k not a multiple of 8
+    assert call(**args(4, 28672, 4096, dt=5)) == _lib.NIMBUS_ERR_UNSUPPORTED
+    for bad in [dict(bm=48), dict(bm=16, ks=8), dict(bm=128, ks=2), dict(bm=64, rw=3), dict(bm=64, ks=3)]:
+        assert call(**args(4, 28672, 4096, **bad)) == _lib.NIMBUS_ERR_UNSUPPORTED, bad
+    assert call(**args(0, 28672, 4096)) == 0  # no rows: nothing to launch
+    assert call(**args(4, 28672, 4096, x=None)) == _lib.NIMBUS_ERR_INVALID
+    assert call(**args(4, 28672, 4096, xs=4088)) == _lib.NIMBUS_ERR_INVALID  # stride below k
+    assert call(**args(4, 28672, 4096, ys=14332)) == _lib.NIMBUS_ERR_INVALID  # stride below n / 2
+    assert call(**args(4, 28672, 4096, x=DUMMY + 1)) == _lib.NIMBUS_ERR_ALIGNMENT
+    assert call(**args(4, 28672, 4096, x=DUMMY + 2)) == _lib.NIMBUS_ERR_ALIGNMENT  # not 16-byte aligned
+    assert call(**args(4, 28672, 4096, s=DUMMY + 4)) == _lib.NIMBUS_ERR_ALIGNMENT
+    assert call(**args(4, 28672, 4096, ys=14338)) == _lib.NIMBUS_ERR_ALIGNMENT  # y stride not a multiple of 4
+
+
 def test_int8_workspace_is_splits_times_fp32_output():
     lib = _lib.load()
     ws = lib.nimbus_int8_matmul_workspace_bytes

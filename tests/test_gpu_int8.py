@@ -285,3 +285,39 @@ def test_split_plan_replays_in_a_graph():
         call()
         torch.cuda.synchronize()
         assert torch.equal(y, want), rep
+
+
+@pytest.mark.parametrize("dtype,n,k", [(torch.float16, 11264, 2048), (torch.bfloat16, 28672, 4096),
+                                       (torch.bfloat16, 96, 200), (torch.float16, 160, 64)])
+@pytest.mark.parametrize("m", [1, 7, 64, 300])
+def test_packed_silu_equals_projection_then_gate(dtype, n, k, m):
+    """The gate_up projection fused with the SiLU gate gives, bit for bit,
+    silu_mul of the projection's output under the same launch plan, for
+    every plan it takes (and its default): TinyLlama's and Llama-3-8B's
+    gate_up shapes, and small ones whose gate half leaves a workgroup's last
+    row-block groups empty (n = 96: 3 gate blocks; n = 160: 5)."""
+    from nimbus_amd.kernels.elementwise import silu_mul
+    from nimbus_amd.kernels.int8_matmul import _silu_plans, int8_matmul_packed_silu
+
+    announce(f"int8 packed silu m={m} n={n} k={k} {dtype}")
+    x, q, s = _case(m, n, k, dtype, seed=m + n)
+    p = pack_int8_weight(q)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    dt = _lib.dtype_code(dtype)
+    for plan in _silu_plans(m, n, k) + [(0, 1, 1)]:
+        fused = torch.full((m, n // 2), 7.0, dtype=dtype, device="cuda")
+        rc = lib.nimbus_int8_matmul_packed_silu(x.data_ptr(), k, p.data_ptr(), s.data_ptr(), fused.data_ptr(),
+                                                n // 2, m, n, k, *plan, dt, stream)
+        assert rc == 0, plan
+        bm, ks, rw = plan if plan[0] else ((16 if m <= 16 else 32 if m <= 32 else 64), 1, 1)
+        y = torch.empty(m, n, dtype=dtype, device="cuda")
+        rc = lib.nimbus_int8_matmul_packed_plan(x.data_ptr(), k, p.data_ptr(), s.data_ptr(), y.data_ptr(), n, m, n,
+                                                k, bm, ks, 1, rw, None, 0, dt, stream)
+        assert rc == 0, plan
+        want = silu_mul(y)
+        assert torch.equal(fused, want), (plan, (fused.float() - want.float()).abs().max().item())
+    # the wrapper (tuned plan) and the INT8 layer's fused path agree with the two steps within rounding
+    got = int8_matmul_packed_silu(x, p, s, n, k)
+    two = silu_mul(int8_matmul_packed(x, p, s, n, k))
+    assert torch.allclose(got.float(), two.float(), atol=2e-2, rtol=1e-2)
