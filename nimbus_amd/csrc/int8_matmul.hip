@@ -1011,13 +1011,14 @@ extern "C" int nimbus_int8_matmul_packed(const void* x, int64_t x_stride, const 
 
 // An explicit plan: token tile bm (16, 32, 64, 128), k slices ks (1, 2, 4,
 // 8; ks * bm <= 128), k splits (1..16, fewer when K is short) and row blocks
-// per wave rw (1, 2). Workspace: splits * m * n * 4 bytes when the plan
-// splits.
+// per wave rw (1, 2). Its token tiles are the grid's z dimension, so there
+// are at most 65535 of them. Workspace: splits * m * n * 4 bytes when the
+// plan splits.
 static bool make_plan(int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks, int32_t splits, int32_t rw,
                       PackPlan* p) {
-  (void)m;
   (void)n;
   if (bm != 16 && bm != 32 && bm != 64 && bm != 128) return false;
+  if ((m + bm - 1) / bm > 65535) return false;
   if (ks != 1 && ks != 2 && ks != 4 && ks != 8) return false;
   if (rw != 1 && rw != 2) return false;
   if (ks * bm > 128 || splits < 1 || splits > kMaxSplits) return false;

@@ -237,6 +237,11 @@ def test_int8_packed_silu_rejects_before_launch():
     for bad in [dict(bm=48), dict(bm=16, ks=8), dict(bm=128, ks=2), dict(bm=64, rw=3), dict(bm=64, ks=3)]:
         assert call(**args(4, 28672, 4096, **bad)) == _lib.NIMBUS_ERR_UNSUPPORTED, bad
     assert call(**args(0, 28672, 4096)) == 0  # no rows: nothing to launch
+    # 65536 token tiles of 16: more than the grid's z dimension takes (65535 of them are still accepted
+    # as a plan: the workspace query answers for it)
+    assert call(**args(16 * 65536, 64, 64, bm=16)) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert lib.nimbus_int8_matmul_packed_plan_workspace_bytes(16 * 65536, 64, 64, 16, 1, 1, 1) == -1
+    assert lib.nimbus_int8_matmul_packed_plan_workspace_bytes(16 * 65535, 64, 64, 16, 1, 1, 1) == 0
     assert call(**args(4, 28672, 4096, x=None)) == _lib.NIMBUS_ERR_INVALID
     assert call(**args(4, 28672, 4096, xs=4088)) == _lib.NIMBUS_ERR_INVALID  # stride below k
     assert call(**args(4, 28672, 4096, ys=14332)) == _lib.NIMBUS_ERR_INVALID  # stride below n / 2
