@@ -368,8 +368,9 @@ int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* 
  * MLP.forward's F.silu(gate) * up over Int8Linear's output
  * (nimbus/model/llama.py:100-103, nimbus/quant/int8.py:43-47): w_packed holds
  * gate_up_proj's n = 2 * intermediate rows (gate rows first), and y [m, n/2]
- * receives what nimbus_silu_mul would make of nimbus_int8_matmul_packed's
- * [m, n] output, bit for bit, without that output being written. n a multiple
+ * receives what nimbus_silu_mul would make of the [m, n] output of
+ * nimbus_int8_matmul_packed_plan under the same plan (bm, ks, one split,
+ * rows_per_wave), bit for bit, without that output being written. n a multiple
  * of 32, k of 8; one split of K: bm (16, 32, 64 or 128; 0 picks from m with
  * ks = 1 and one row block per wave), ks (1, 2 or 4, ks * bm <= 128) and
  * rows_per_wave (1 or 2) as for nimbus_int8_matmul_packed_plan. The tiled

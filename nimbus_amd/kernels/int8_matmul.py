@@ -282,11 +282,13 @@ def _tune_silu(x2, w_packed, scale, y, n, k, lib) -> tuple[int, int, int] | None
 
 def int8_matmul_packed_silu(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor, n: int, k: int,
                             out: torch.Tensor | None = None) -> torch.Tensor:
-    """silu_mul(int8_matmul_packed(x, w_packed, scale, n, k)) in one launch,
-    bit for bit (the MLP's gate_up projection and SiLU gate,
-    nimbus/model/llama.py:100-103): [..., n / 2]. n a multiple of 32 (gate
-    rows first, then up rows); the plan is tuned per shape as
-    int8_matmul_packed's is."""
+    """silu_mul(int8_matmul_packed(x, w_packed, scale, n, k)) in one launch
+    (the MLP's gate_up projection and SiLU gate, nimbus/model/llama.py:
+    100-103): [..., n / 2]. n a multiple of 32 (gate rows first, then up
+    rows). Under one launch plan the result is the two steps' bit for bit;
+    the plan is tuned per shape as int8_matmul_packed's is, but apart from
+    it, so where the two pick plans with other k slices the sums over K
+    differ in fp32 order (results within rounding)."""
     if w_packed.dtype != torch.int8 or w_packed.shape != (-(-n // 16), -(-k // 64), 1024):
         raise ValueError("w_packed must be pack_int8_weight's layout for [n, k]")
     if n % 32 != 0:

@@ -128,7 +128,8 @@ class MLP(nn.Module):
 
     def forward(self, x):
         # An INT8 gate_up projection runs with the SiLU gate in its epilogue
-        # (the same bits as the two steps, one launch and no [M, 2I] output).
+        # (one launch and no [M, 2I] output; the two steps' bits under the
+        # same launch plan).
         fused = getattr(self.gate_up_proj, "forward_silu", None)
         h = fused(x) if fused is not None else None
         if h is None:

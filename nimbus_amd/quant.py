@@ -59,9 +59,10 @@ class Int8Linear(nn.Module):
         return int8_matmul_packed(x, self.weight_packed, self.scale, self.out_features, self.in_features)
 
     def forward_silu(self, x: torch.Tensor) -> torch.Tensor | None:
-        """silu_mul(self(x)) in one launch, bit for bit, for the MLP's gate_up
-        projection (gate rows first); None when out_features is not a
-        multiple of 32 (the caller then runs the two steps)."""
+        """silu_mul(self(x)) in one launch, for the MLP's gate_up projection
+        (gate rows first): bit for bit under the same launch plan, within
+        rounding where the two tune different ones; None when out_features
+        is not a multiple of 32 (the caller then runs the two steps)."""
         if self.out_features % 32 != 0:
             return None
         return int8_matmul_packed_silu(x, self.weight_packed, self.scale, self.out_features, self.in_features)

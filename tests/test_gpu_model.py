@@ -12,7 +12,9 @@ graphs and the on-device greedy chain.
 - greedy_chain against step-by-step graph runs with host argmax: identical
   tokens (the same kernels), and every graph replay equals the eager call.
 - The INT8-quantized model stays close to the unquantized one
-  (nimbus's test_quantized_tiny_model_stays_close: cosine > 0.99).
+  (nimbus's test_quantized_tiny_model_stays_close: cosine > 0.99); its
+  MLP (gate_up with the SiLU gate in the epilogue) equals the separate
+  launches within rounding, and its decode graphs match its eager steps.
 - The rotary, SiLU and greedy-step kernels against torch.
 """
 
@@ -278,6 +280,39 @@ def test_int8_model_stays_close():
             s.feed(t)
         batch = [(s, 1) for s in seqs]
         q_batch = [(s, 1) for s in q_seqs]
+
+
+@pytest.mark.parametrize("n,dtype", [(5, torch.bfloat16), (16, torch.float16)])
+def test_int8_decode_graphs_match_eager(n, dtype):
+    """The INT8-quantized model, whose MLP runs the gate_up projection with
+    the SiLU gate in its epilogue: its MLP equals the projection, then
+    silu_mul, then down_proj, within rounding (each wrapper tunes its own
+    launch plan, so the sums over K may be added in another order; under
+    one plan the two are equal bit for bit, tests/test_gpu_int8.py); its
+    decode steps replayed from DecodeGraphs give the eager steps' greedy
+    tokens and logits within rounding."""
+    announce(f"int8 decode graphs n={n} {dtype}")
+    model, caches, seqs = _setup(dtype, [3 + 7 * i for i in range(n)], num_blocks=160, seed=40 + n)
+    quantize_model(model)
+    mlp = model.layers[0].mlp
+    x = torch.randn(n, CFG.hidden_size, device="cuda").to(dtype)
+    assert mlp.gate_up_proj.forward_silu(x) is not None  # the fused path is the one MLP.forward takes
+    torch.testing.assert_close(mlp(x), mlp.down_proj(silu_mul(mlp.gate_up_proj(x))), atol=1e-2, rtol=1e-2)
+    _prefill(model, caches, seqs)
+    g_seqs, e_seqs = _clone_seqs(seqs), _clone_seqs(seqs)
+    g_caches, e_caches = _clone_caches(caches), _clone_caches(caches)
+    graphs = DecodeGraphs(model, g_caches, BS, max_model_len=512, max_batch=16, scratch_block=160,
+                          num_kv_heads=CFG.num_kv_heads, device="cuda")
+    graphs.capture()
+    for step_i in range(4):
+        got = graphs.run(g_seqs).clone()
+        _, want = _eager_step(model, e_caches, [(s, 1) for s in e_seqs])
+        torch.testing.assert_close(got, want, atol=1e-2, rtol=1e-2)
+        g_tok, e_tok = got.argmax(-1).tolist(), want.argmax(-1).tolist()
+        assert g_tok == e_tok, (step_i, g_tok, e_tok)
+        for ss in (g_seqs, e_seqs):
+            for s, t in zip(ss, e_tok):
+                s.feed(t)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
