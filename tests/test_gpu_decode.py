@@ -111,6 +111,31 @@ def test_largest_batch():
     assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, scale, batched=True), what="vs oracle")
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_decode_batches_match_oracle(seed):
+    """Seeded random batches: head shapes with GQA groups of 1-32, D 64 or
+    128, both dtypes, 1-300 sequences with log-uniform contexts of 1-12,000
+    tokens and a few on page edges, pages scattered over the pool."""
+    import numpy as np
+
+    rng = np.random.default_rng(1000 + seed)
+    shapes = [(32, 8), (32, 4), (16, 16), (28, 4), (32, 1), (64, 8), (8, 8), (40, 8), (56, 8), (32, 2)]
+    heads, kv = shapes[int(rng.integers(len(shapes)))]
+    d = int(rng.choice([64, 128]))
+    dtype = [torch.float16, torch.bfloat16][seed % 2]
+    b = max(1, int(np.exp(rng.uniform(0, np.log(300)))))
+    ctx = [max(1, int(np.exp(rng.uniform(0, np.log(12000))))) for _ in range(b)]
+    for _ in range(min(b, 4)):
+        ctx[int(rng.integers(b))] = max(1, int(16 * rng.integers(1, 200) + rng.integers(-1, 2)))
+    announce(f"decode random batch seed={seed} H={heads} KV={kv} D={d} {dtype} B={b} sum_ctx={sum(ctx)}")
+    batch = workloads.build_batch([(c, 1) for c in ctx], heads=heads, kv_heads=kv, head_dim=d, dtype=dtype,
+                                  device="cuda", seed=seed, fill="used")
+    da = batch.decode_args()
+    got = paged_decode_attention(*da)
+    want = oracle_decode(da[0], batch.k_cache, batch.v_cache, batch.decode_context_host(), da[4], batch.scale)
+    assert_within(got.cpu(), want, what="vs oracle")
+
+
 def test_grid_width_does_not_change_results():
     """A wider grid (larger max_context, as under graph capture) only adds
     partitions that exit at once: results are bit-identical."""
