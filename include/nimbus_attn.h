@@ -220,10 +220,11 @@ int nimbus_paged_prefill_pieces(const void* q, int64_t q_stride_t, int64_t q_str
  * first folding in the pieces of shares [fix_lo, fix_hi), which must be
  * lower than its own (it waits for each to be written), and writes out.
  * Workspace: nimbus_paged_prefill_stream_workspace_bytes(); its first
- * nimbus_paged_prefill_stream_flag_bytes() must be zero before the first
- * call (flags, then an error word), and a completed call leaves them zero
- * (the error word aside, which turns nonzero if a wait ever gives up on an
- * inconsistent plan). Calls sharing a workspace must not overlap.
+ * nimbus_paged_prefill_stream_flag_bytes() (the same for every plan, so
+ * calls with different plans may share a workspace) must be zero before the
+ * first call (flags, then an error word), and a completed call leaves them
+ * zero (the error word aside, which turns nonzero if a wait ever gives up on
+ * an inconsistent plan). Calls sharing a workspace must not overlap.
  * Replaces the same reference interface as nimbus_paged_prefill
  * (nimbus/kernels/prefill_attention.py:93-119); the plan stands in for the
  * tile table of build_programs (prefill_attention.py:81-90).

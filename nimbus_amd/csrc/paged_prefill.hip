@@ -173,6 +173,15 @@ enum SkField : int { kSkSeq = 0, kSkM0, kSkKb0, kSkKb1, kSkSlot, kSkFixLo, kSkFi
 // (the contributors it waits on are lower-numbered workgroups, dispatched
 // before it, so a wait ends unless the plan is inconsistent).
 constexpr int kSkMaxPolls = 1 << 22;
+// Stream-K workspace layout, the same for every plan: a flag word per (share,
+// kv-head group, wave) for the most workgroups a call accepts, then an error
+// word (in a 256-byte line of its own), then the split pieces' slots. Flags
+// sized to the plan would let one plan's slots lie where another plan's
+// flags do, so a workspace shared by calls with different plans would start
+// a call with nonzero "flags" (stale partials), and a fix-up would fold in
+// pieces not yet written.
+constexpr int64_t kSkMaxWorkgroups = 2048;                 // shares x kv-head groups (two per CU: 1,024 CUs)
+constexpr int64_t kSkFlagBytes = kSkMaxWorkgroups * 4 * 4;  // four waves a workgroup at most, a word each
 
 // SK: the workgroup walks the pieces of its stream-K share (one kv-head
 // group, the share's list of (unit, key-block range) pieces); otherwise it
@@ -960,10 +969,12 @@ static int prefill_impl(const void* q, int64_t q_stride_t, int64_t q_stride_h, c
     int64_t cus = 0;
     const int e = device_cus(&cus);
     if (e != 0) return e;
-    if (static_cast<int64_t>(num_units) * a.kvg > 2 * cus) return NIMBUS_ERR_UNSUPPORTED;
+    if (static_cast<int64_t>(num_units) * a.kvg > 2 * cus ||
+        static_cast<int64_t>(num_units) * a.kvg > kSkMaxWorkgroups)
+      return NIMBUS_ERR_UNSUPPORTED;
     const int waves = gs == 1 ? 2 : 4;
     const int64_t slots = static_cast<int64_t>(num_units) * a.kvg * waves;
-    const int64_t flag_bytes = (slots * 4 + 255) / 256 * 256;
+    const int64_t flag_bytes = kSkFlagBytes;
     const int64_t need = flag_bytes + 256 + slots * (head_dim / 32 * 16 + 2) * 64 * 4;
     if (workspace == nullptr || workspace_bytes < need) return NIMBUS_ERR_WORKSPACE;
     if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0) return NIMBUS_ERR_ALIGNMENT;
@@ -1033,7 +1044,8 @@ extern "C" int nimbus_paged_prefill_pieces(const void* q, int64_t q_stride_t, in
 }
 
 // Stream-K workspace: the flags (zero before the first call; every call that
-// completes leaves them zero), an error word, then the split pieces' slots.
+// completes leaves them zero) and the error word, at the same offsets for
+// every plan, then the split pieces' slots.
 static int64_t stream_slots(int32_t shares, int32_t num_heads, int32_t num_kv_heads) {
   const int G = num_heads / num_kv_heads;
   const int gs = G % 8 == 0 ? 8 : (G % 4 == 0 ? 4 : (G % 2 == 0 ? 2 : 1));
@@ -1043,7 +1055,7 @@ static int64_t stream_slots(int32_t shares, int32_t num_heads, int32_t num_kv_he
 extern "C" int64_t nimbus_paged_prefill_stream_flag_bytes(int32_t num_shares, int32_t num_heads,
                                                           int32_t num_kv_heads) {
   if (num_shares < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0) return -1;
-  return (stream_slots(num_shares, num_heads, num_kv_heads) * 4 + 255) / 256 * 256 + 256;
+  return kSkFlagBytes + 256;
 }
 
 extern "C" int64_t nimbus_paged_prefill_stream_workspace_bytes(int32_t num_shares, int32_t num_heads,

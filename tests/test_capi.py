@@ -251,6 +251,19 @@ def test_int8_packed_silu_rejects_before_launch():
     assert call(**args(4, 28672, 4096, ys=14338)) == _lib.NIMBUS_ERR_ALIGNMENT  # y stride not a multiple of 4
 
 
+def test_stream_flag_area_is_the_same_for_every_plan():
+    """The stream-K workspace keeps its flags and error word at the same
+    offsets whatever the plan, so calls with different plans can share one
+    workspace; the slots after them grow with the plan."""
+    lib = _lib.load()
+    fb = lib.nimbus_paged_prefill_stream_flag_bytes
+    ws = lib.nimbus_paged_prefill_stream_workspace_bytes
+    sizes = {fb(s, h, kv) for s, h, kv in [(1, 8, 8), (128, 32, 1), (64, 32, 8), (512, 64, 8), (7, 28, 4)]}
+    assert len(sizes) == 1 and sizes.pop() > 0
+    assert fb(-1, 32, 8) == -1 and fb(4, 30, 8) == -1
+    assert fb(4, 32, 8) < ws(4, 32, 8, 64) < ws(8, 32, 8, 64) < ws(8, 32, 8, 128)
+
+
 def test_int8_workspace_is_splits_times_fp32_output():
     lib = _lib.load()
     ws = lib.nimbus_int8_matmul_workspace_bytes

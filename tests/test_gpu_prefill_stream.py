@@ -81,6 +81,32 @@ def test_stream_cut_units_and_whole_prompts(dtype, seqs):
     assert_within(got.cpu()[rows], tile.cpu()[rows].double(), what="stream vs tile kernel")
 
 
+def test_stream_plans_of_different_shapes_share_one_workspace():
+    """Calls whose plans differ (head shapes, head dims, share counts) one
+    after another on one workspace, twice round: each matches the oracle, the
+    flags are back at zero and the error word stays zero after every call.
+    (Flag areas sized to the plan once let a call's partial slots lie where a
+    later plan's flags did, and that later call folded in stale pieces.)"""
+    cases = [((32, 8, 128), [(512, 1343), (512, 599), (300, 900), (64, 5000)], torch.bfloat16, 512),
+             ((32, 1, 64), [(199, 199), (540, 540)], torch.bfloat16, 512),
+             ((32, 2, 64), [(542, 5223), (83, 83), (302, 302), (665, 4735)], torch.float16, 512),
+             ((32, 4, 128), [(212, 2633), (629, 6031), (456, 456)], torch.float16, 64)]
+    built = []
+    for i, ((heads, kv, d), seqs, dtype, resident) in enumerate(cases):
+        q, k, v, qst, ctxt, bt, scale, qs, ctx = _case(heads, kv, d, seqs, dtype, seed=30 + i)
+        plan = plan_stream(qs, ctx, heads, kv, "cuda", resident=resident)
+        built.append((heads, kv, d, plan, (q, k, v, qst, ctxt, bt, scale, qs, ctx),
+                      oracle_prefill(q, k, v, qs, ctx, bt, scale)))
+    ws = new_stream_workspace(max(stream_workspace_bytes(b[3].num_shares, b[0], b[1], b[2]) for b in built), "cuda")
+    for rnd in range(2):
+        for heads, kv, d, plan, args, want in built:
+            announce(f"prefill stream shared workspace round {rnd} H={heads} KV={kv} D={d} shares={plan.num_shares}")
+            got = paged_prefill_attention(*args, plan, workspace=ws)
+            torch.cuda.synchronize()
+            assert stream_error(ws, plan.num_shares, heads, kv) == 0 and _flags_clear(ws, plan, heads, kv)
+            assert_within(got.cpu(), want, what=f"H={heads} KV={kv} D={d} round {rnd}")
+
+
 @pytest.mark.parametrize("config", ["tinyllama_prefill", "llama3_mixed"])
 def test_stream_configs_full(config):
     announce(f"prefill stream config {config}")
