@@ -321,3 +321,36 @@ def test_packed_silu_equals_projection_then_gate(dtype, n, k, m):
     got = int8_matmul_packed_silu(x, p, s, n, k)
     two = silu_mul(int8_matmul_packed(x, p, s, n, k))
     assert torch.allclose(got.float(), two.float(), atol=2e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_shapes_are_exact_on_small_integers(seed):
+    """Seeded random shapes (1-700 tokens; any N and K, and multiples of 32
+    and 64) on small-integer activations, where every fp32 sum is exact: the
+    row-major kernel, the packed kernel under its tuned plan and, for N a
+    multiple of 32, the fused gate_up + SiLU all give the reference formula's
+    bits (the fused one silu_mul's of the exact projection)."""
+    import numpy as np
+
+    from nimbus_amd.kernels.elementwise import silu_mul
+    from nimbus_amd.kernels.int8_matmul import int8_matmul_packed_silu
+
+    rng = np.random.default_rng(4000 + seed)
+    dtype = [torch.float16, torch.bfloat16][seed % 2]
+    m = int(np.exp(rng.uniform(0, np.log(700))))
+    n = int(rng.choice([int(rng.integers(1, 9000)), 32 * int(rng.integers(1, 300))]))
+    k = int(rng.choice([int(rng.integers(1, 6000)), 64 * int(rng.integers(1, 90))]))
+    announce(f"int8 random shape seed={seed} m={m} n={n} k={k} {dtype}")
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randint(-4, 5, (m, k), generator=g).to(dtype)
+    wq = torch.randint(-127, 128, (n, k), generator=g).to(torch.int8)
+    sc = (torch.rand(n, generator=g) * 0.01 + 1e-4).to(dtype)
+    want = reference.int8_matmul(x, wq, sc)
+    xd, wd, sd = x.cuda(), wq.cuda(), sc.cuda()
+    assert torch.equal(int8_matmul(xd, wd, sd).cpu(), want)
+    if k % 8 == 0:
+        packed = pack_int8_weight(wd)
+        assert torch.equal(int8_matmul_packed(xd, packed, sd, n, k).cpu(), want)
+        if n % 32 == 0:
+            fused = int8_matmul_packed_silu(xd, packed, sd, n, k)
+            assert torch.equal(fused.cpu(), silu_mul(want.cuda()).cpu())
