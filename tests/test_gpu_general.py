@@ -10,7 +10,8 @@ Decode, verify and varlen prefill calls are checked against the oracle
 and 256 (and 128 on 32-token pages), GQA groups 1-32 (at 32 the heads of a
 kv head split over several workgroups), both dtypes; contexts
 at and around page edges, rows longer than the block table covers cut to
-it, and a graph-captured decode call that replays bit for bit.
+it, and a graph-captured decode call that replays bit for bit; and six
+seeded random shapes (head dims 16-256, pages of 1-64 tokens).
 """
 
 from __future__ import annotations
@@ -181,3 +182,38 @@ def test_backend_step_on_32_token_pages():
                                                     bt[:len(prefills)], d ** -0.5), what="prefill part")
     assert_within(out[n_pre:].cpu(), oracle_decode(q[n_pre:], k_cache, v_cache, decodes, bt[len(prefills):],
                                                    d ** -0.5), what="decode part")
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_general_random_shapes_match_oracle(seed):
+    """Seeded random shapes the general kernel takes: head dims 16-256,
+    pages of 1-64 tokens, GQA groups 1-32, both dtypes; decode over 1-24
+    log-uniform contexts up to 4,000 tokens, and prefill chunks over
+    prefixes, against the oracle."""
+    import numpy as np
+
+    rng = np.random.default_rng(7000 + seed)
+    kv = int(rng.choice([1, 2, 4, 8]))
+    heads = kv * int(rng.choice([1, 2, 3, 4, 5, 7, 8, 16, 32]))
+    d = int(rng.choice([16, 32, 48, 64, 80, 96, 112, 128, 160, 192, 256]))
+    bs = int(rng.choice([1, 2, 4, 8, 16, 32, 64]))
+    if bs == 16 and d in (64, 128):
+        bs = 32  # (the tuned kernels' shape)
+    dtype = [torch.float16, torch.bfloat16][seed % 2]
+    n = int(rng.integers(1, 24))
+    ctx_lens = [max(1, int(np.exp(rng.uniform(0, np.log(4000))))) for _ in range(n)]
+    announce(f"general random seed={seed} H={heads} KV={kv} D={d} bs={bs} {dtype} n={n}")
+    k, v, bt = _cache(kv, d, bs, ctx_lens, dtype, seed=seed)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(n, heads, d, generator=g, device="cuda").to(dtype)
+    ctx = torch.tensor(ctx_lens, dtype=torch.int32, device="cuda")
+    got = paged_decode_attention(q, k, v, ctx, bt, max(ctx_lens), d ** -0.5)
+    assert_within(got.cpu(), oracle_decode(q, k, v, ctx_lens, bt, d ** -0.5), what="general decode vs oracle")
+    q_lens = [int(rng.integers(1, 300)) for _ in range(min(n, 6))]
+    p_lens = [ql + int(rng.choice([0, int(rng.integers(1, 1500))])) for ql in q_lens]
+    k, v, bt = _cache(kv, d, bs, p_lens, dtype, seed=seed + 1)
+    qs = query_starts(q_lens)
+    qp = torch.randn(qs[-1], heads, d, generator=g, device="cuda").to(dtype)
+    got = paged_prefill_attention(qp, k, v, torch.tensor(qs, dtype=torch.int32, device="cuda"),
+                                  torch.tensor(p_lens, dtype=torch.int32, device="cuda"), bt, d ** -0.5, qs, p_lens)
+    assert_within(got.cpu(), oracle_prefill(qp, k, v, qs, p_lens, bt, d ** -0.5), what="general prefill vs oracle")
