@@ -422,6 +422,7 @@ __global__ __launch_bounds__(kGemmThreads) void int8_matmul_packed_kernel(GemmAr
   const int kchunks = (a.K + 63) / 64;
   constexpr int HRB = RB / 2;
   static_assert(!SILU || RB % 2 == 0, "gate and up row blocks pair up");
+  static_assert(!SILU || (RB / 2) * RW * CB * 64 * 8 <= kXBufs * XBUF, "the up rows' outputs fit the x buffers");
   const int hb = a.N / 32;  // gate row blocks (SILU)
   int nb0;
   if constexpr (SILU) nb0 = rb < HRB ? (blockIdx.x * HRB + rb) * RW : hb + (blockIdx.x * HRB + rb - HRB) * RW;
