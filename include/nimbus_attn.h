@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define NIMBUS_ATTN_ABI_VERSION 14
+#define NIMBUS_ATTN_ABI_VERSION 15
 
 /* dtype codes */
 #define NIMBUS_FLOAT16 0
@@ -297,6 +297,26 @@ int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* residual, i
                         void* stream);
 
 /*
+ * nimbus_add_rms_norm where x is an INT8 projection's output still in split-K
+ * partials: partials [splits][rows][cols] fp32 as
+ * nimbus_int8_matmul_packed_partials leaves them and scale [cols] the
+ * projection's channel scales. Each x element is formed as the projection's
+ * reducing launch forms it (the partials summed in split order, times the
+ * scale in fp32, rounded to the element type), so out and residual_out are
+ * bit for bit those of nimbus_int8_matmul_packed_plan (same plan) followed by
+ * nimbus_add_rms_norm. A residual is required; cols a multiple of 8, at most
+ * 8192; every pointer 16-byte aligned, row strides multiples of 8. Has no
+ * counterpart call in the reference: it folds the projection's reduction into
+ * the norm that reads its output next (nimbus/model/llama.py:115-124, around
+ * the o_proj and down_proj of nimbus/quant/int8.py's Int8Linear), one launch
+ * instead of two.
+ */
+int nimbus_add_rms_norm_partials(const float* partials, int32_t splits, const void* scale, const void* residual,
+                                 int64_t residual_stride, const void* weight, void* out, int64_t out_stride,
+                                 void* residual_out, int64_t residual_out_stride, int64_t rows, int32_t cols,
+                                 float eps, int32_t dtype, void* stream);
+
+/*
  * Bytes of workspace nimbus_int8_matmul needs for an [m, k] x [n, k]^T
  * product (0 when it runs without one): a pure function of the shape. The
  * workspace carries nothing between calls; concurrent calls need their own.
@@ -381,6 +401,21 @@ int nimbus_int8_matmul_packed_plan(const void* x, int64_t x_stride, const void* 
 int nimbus_int8_matmul_packed_silu(const void* x, int64_t x_stride, const void* w_packed, const void* scale, void* y,
                                    int64_t y_stride, int64_t m, int32_t n, int32_t k, int32_t bm, int32_t ks,
                                    int32_t rows_per_wave, int32_t dtype, void* stream);
+
+/*
+ * The first half of nimbus_int8_matmul_packed_plan for a plan that splits K
+ * (splits >= 2 once the plan is made; NIMBUS_ERR_UNSUPPORTED otherwise): the
+ * per-split fp32 sums land in workspace as [splits][m][n]
+ * (nimbus_int8_matmul_packed_plan_workspace_bytes() bytes) and no reducing
+ * launch follows, for a consumer that folds them in
+ * (nimbus_add_rms_norm_partials). Arguments as for
+ * nimbus_int8_matmul_packed_plan, less scale and y. Replaces the same
+ * reference interface (Int8Linear.forward, nimbus/quant/int8.py:43-47),
+ * whose output the next call completes.
+ */
+int nimbus_int8_matmul_packed_partials(const void* x, int64_t x_stride, const void* w_packed, int64_t m, int32_t n,
+                                       int32_t k, int32_t bm, int32_t ks, int32_t splits, int32_t rows_per_wave,
+                                       void* workspace, int64_t workspace_bytes, int32_t dtype, void* stream);
 
 /*
  * Rotary position embedding, in place. Replaces Rotary.forward

@@ -27,7 +27,7 @@ NIMBUS_ERR_ALIGNMENT = -3
 NIMBUS_ERR_WORKSPACE = -4
 NIMBUS_ERR_SCRATCH = -5
 NOALLOC_SCRATCH_BYTES = 64 << 20  # NIMBUS_NOALLOC_SCRATCH_BYTES
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 # Entry points and their C signatures, in the order include/nimbus_attn.h declares them.
 _c_int, _c_i32, _c_i64, _c_p, _c_f = ctypes.c_int, ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_float
@@ -62,6 +62,8 @@ SIGNATURES = {
     "nimbus_paged_verify": None,
     "nimbus_add_rms_norm": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64, _c_i64, _c_i32,
                                      _c_f, _c_i32, _c_p]),
+    "nimbus_add_rms_norm_partials": (_c_int, [_c_p, _c_i32, _c_p, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_p, _c_i64,
+                                              _c_i64, _c_i32, _c_f, _c_i32, _c_p]),
     "nimbus_int8_matmul_workspace_bytes": (_c_i64, [_c_i64, _c_i32, _c_i32]),
     "nimbus_int8_matmul": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p,
                                     _c_i64, _c_i32, _c_p]),
@@ -76,6 +78,8 @@ SIGNATURES = {
                                                 _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_p]),
     "nimbus_int8_matmul_packed_silu": (_c_int, [_c_p, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_i64, _c_i32, _c_i32,
                                                 _c_i32, _c_i32, _c_i32, _c_i32, _c_p]),
+    "nimbus_int8_matmul_packed_partials": (_c_int, [_c_p, _c_i64, _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
+                                                    _c_i32, _c_i32, _c_p, _c_i64, _c_i32, _c_p]),
     "nimbus_rope": (_c_int, [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_p]),
     "nimbus_rope_write_kv": (_c_int, [_c_p, _c_i64, _c_i64, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_p, _c_i64, _c_i32,
                                       _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_p]),

@@ -29,6 +29,7 @@
 
 #include "common.h"
 #include "nimbus_attn_internal.h"
+#include "int8_epilogue.h"
 #include "silu.h"
 
 namespace nimbus {
@@ -77,22 +78,6 @@ __device__ __forceinline__ int x_chunk(int t, int c) {
 __device__ __forceinline__ int x_chunk_at(int t, int p) {
   const int u = p ^ (t & 7);
   return ((u << 1) & 6) | (u >> 2);
-}
-
-// dtype(acc * scale) as the reference forms it: the fp32 product, then the
-// conversion to the 16-bit type. Left to itself the compiler turns some of
-// these into one v_fma_mixlo_f16 (the exact product rounded to 16 bits once)
-// and others into a multiply and a conversion, picking per element and per
-// kernel: about one output in 10^4 then differs by an ulp between two
-// kernels that store the same value (measured on the fused gate_up + SiLU
-// launch against the projection and the gate run apart). The empty asm keeps
-// the fp32 product in a register, so every store rounds twice, as the
-// reference does.
-template <int DT>
-__device__ __forceinline__ uint16_t scaled(float acc, float scale) {
-  float p = acc * scale;
-  asm volatile("" : "+v"(p));
-  return Elem<DT>::from_f32(p);
 }
 
 // Eight int8 (two dwords) -> the eight fp16 / bf16 of an MFMA operand.
@@ -757,7 +742,7 @@ static int launch_packed(const GemmArgs& a, hipStream_t s) {
   }
   const dim3 grid(((a.N + 15) / 16 + RB * RW - 1) / (RB * RW), a.splits, (a.M + BM - 1) / BM);
   hipLaunchKernelGGL((int8_matmul_packed_kernel<DT, BM, KS, RW, false>), grid, dim3(kGemmThreads), 0, s, a);
-  if (a.splits > 1) {
+  if (a.splits > 1 && a.y) {  // (no y: the caller folds the partials in itself)
     const int64_t quads = static_cast<int64_t>(a.M) * (a.N / 4);
     hipLaunchKernelGGL((int8_matmul_reduce_kernel<DT>), dim3(static_cast<unsigned>((quads + 255) / 256)), dim3(256),
                        0, s, a);
@@ -1107,4 +1092,50 @@ extern "C" int nimbus_int8_matmul_packed_silu(const void* x, int64_t x_stride, c
   a.ksplit = p.ksplit;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return dtype == kFloat16 ? launch_packed_dt<kFloat16, true>(a, p, s) : launch_packed_dt<kBFloat16, true>(a, p, s);
+}
+
+// The split-K partials of a packed-weight projection, without the reducing
+// launch: workspace [splits][m][n] fp32 receives each split's sum over its
+// part of K, in the layout int8_matmul_reduce_kernel reads, for a consumer
+// that folds them in itself (nimbus_add_rms_norm_partials). The plan must
+// split K (splits >= 2 after make_plan).
+extern "C" int nimbus_int8_matmul_packed_partials(const void* x, int64_t x_stride, const void* w_packed, int64_t m,
+                                                  int32_t n, int32_t k, int32_t bm, int32_t ks, int32_t splits,
+                                                  int32_t rows_per_wave, void* workspace, int64_t workspace_bytes,
+                                                  int32_t dtype, void* stream) {
+  if (m < 0 || n <= 0 || k <= 0) return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  PackPlan p;
+  if (!packed_shape_ok(n, k) || !make_plan(m, n, k, bm, ks, splits, rows_per_wave, &p) || p.splits < 2)
+    return NIMBUS_ERR_UNSUPPORTED;
+  if (m == 0) return NIMBUS_OK;
+  if (!x || !w_packed) return NIMBUS_ERR_INVALID;
+  if (x_stride < k) return NIMBUS_ERR_INVALID;
+  const int64_t x_bytes = ((m - 1) * x_stride + k) * 2;
+  const int64_t w_bytes = packed_bytes(n, k);
+  if (m > (int64_t{1} << 21) || x_bytes >= (int64_t{1} << 31) || w_bytes >= (int64_t{1} << 31))
+    return NIMBUS_ERR_UNSUPPORTED;
+  if (x_stride % 8 != 0 || (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w_packed)) % 16 != 0)
+    return NIMBUS_ERR_ALIGNMENT;
+  const int64_t need = static_cast<int64_t>(p.splits) * m * n * 4;
+  if (workspace == nullptr || workspace_bytes < need) return NIMBUS_ERR_WORKSPACE;
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) return NIMBUS_ERR_ALIGNMENT;
+  GemmArgs a;
+  a.x = static_cast<const uint16_t*>(x);
+  a.sx = static_cast<int32_t>(x_stride);
+  a.w = static_cast<const int8_t*>(w_packed);
+  a.sw = 0;
+  a.x_bytes = static_cast<int32_t>(x_bytes);
+  a.w_bytes = static_cast<int32_t>(w_bytes);
+  a.scale = nullptr;
+  a.y = nullptr;
+  a.sy = 0;
+  a.part = static_cast<float*>(workspace);
+  a.M = static_cast<int32_t>(m);
+  a.N = n;
+  a.K = k;
+  a.splits = p.splits;
+  a.ksplit = p.ksplit;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == kFloat16 ? launch_packed_dt<kFloat16, false>(a, p, s) : launch_packed_dt<kBFloat16, false>(a, p, s);
 }

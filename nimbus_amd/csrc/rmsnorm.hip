@@ -17,6 +17,7 @@
 // HBM traffic per row: read x (and r), write out (and the new residual); the
 // weight is read by every row but stays in L2.
 #include "common.h"
+#include "int8_epilogue.h"
 #include "nimbus_attn_internal.h"
 
 namespace nimbus {
@@ -35,6 +36,13 @@ struct NormArgs {
   int64_t sro;
   int32_t rows, cols;
   float eps;
+  // PART: x is an INT8 projection's split-K partials, [splits][rows][cols]
+  // fp32, folded in here as its reducing launch would: summed in split order,
+  // times the channel scale, rounded to the model dtype.
+  const float* part;
+  int64_t plane;
+  int32_t splits;
+  const uint16_t* pscale;
 };
 
 __device__ __forceinline__ float wave_sum(float x) {
@@ -78,7 +86,9 @@ __device__ __forceinline__ uint32_t pack_pair<kBFloat16>(f32x2 v) {
 // serialise the round trips). Stores are nontemporal (streamed past the L2;
 // nothing here reads them again): 8.2 -> 6.9 us at 2048 x 2048 fp16,
 // unchanged at 2108 x 4096 bf16 and 64 rows.
-template <int DT, int NCH, bool RES>
+constexpr int kFold = 4;  // split-K partials of a chunk loaded at once (PART)
+
+template <int DT, int NCH, bool RES, bool PART>
 __global__ __launch_bounds__(256) void add_rms_norm_kernel(NormArgs a) {
   const int wave = static_cast<int>(threadIdx.x) / 64;
   const int lane = threadIdx.x % 64;
@@ -96,8 +106,61 @@ __global__ __launch_bounds__(256) void add_rms_norm_kernel(NormArgs a) {
 #pragma unroll
     for (int c = 0; c < NCH; ++c) {
       if (on[c]) {
-        xw[c] = *reinterpret_cast<const u32x4*>(a.x + static_cast<int64_t>(row) * a.sx + 8 * cidx[c]);
+        if constexpr (!PART) xw[c] = *reinterpret_cast<const u32x4*>(a.x + static_cast<int64_t>(row) * a.sx + 8 * cidx[c]);
         if constexpr (RES) rw[c] = *reinterpret_cast<const u32x4*>(a.r + static_cast<int64_t>(row) * a.sr + 8 * cidx[c]);
+      }
+    }
+    if constexpr (PART) {
+      // The projection's output chunks, bit for bit as its reducing launch
+      // would store them (int8_matmul_reduce_kernel: the splits summed in
+      // order, times the scale, rounded). kFold splits' loads of every chunk
+      // go out together before any is added: one load round trip per kFold
+      // splits instead of per split (64 x 4096 bf16, per call in a graph of
+      // back-to-back calls: 4 splits 6.85 -> 6.17 us, 8 splits 11.4 -> 9.3 us;
+      // the plain norm 4.2 us, the reducing launch this replaces ~4.5 us).
+      const float* base = a.part + static_cast<int64_t>(row) * a.cols;
+      f32x4 lo[NCH], hi[NCH];
+      for (int k0 = 0; k0 < a.splits; k0 += kFold) {
+        f32x4 l[NCH][kFold], h[NCH][kFold];
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+          for (int j = 0; j < kFold; ++j) {
+            if (on[c] && k0 + j < a.splits) {
+              const float* p = base + (k0 + j) * a.plane + 8 * cidx[c];
+              l[c][j] = *reinterpret_cast<const f32x4*>(p);
+              h[c][j] = *reinterpret_cast<const f32x4*>(p + 4);
+            }
+          }
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) {
+#pragma unroll
+          for (int j = 0; j < kFold; ++j) {
+            if (on[c] && k0 + j < a.splits) {
+              if (k0 + j == 0) {
+                lo[c] = l[c][j];
+                hi[c] = h[c][j];
+              } else {
+                lo[c] += l[c][j];
+                hi[c] += h[c][j];
+              }
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) {
+        if (on[c]) {
+          const u32x4 sw = *reinterpret_cast<const u32x4*>(a.pscale + 8 * cidx[c]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const f32x4& v = e < 2 ? lo[c] : hi[c];
+            const int i = 2 * (e % 2);
+            xw[c][e] = pack2(scaled<DT>(v[i], Elem<DT>::to_f32(static_cast<uint16_t>(sw[e]))),
+                             scaled<DT>(v[i + 1], Elem<DT>::to_f32(static_cast<uint16_t>(sw[e] >> 16))));
+          }
+        }
       }
     }
   };
@@ -173,10 +236,12 @@ constexpr int kNormGrid = 1536;
 template <int DT, int NCH>
 static int launch_norm_nch(const NormArgs& a, hipStream_t s) {
   const unsigned grid = static_cast<unsigned>(a.rows < kNormGrid ? a.rows : kNormGrid);
-  if (a.r) {
-    hipLaunchKernelGGL((add_rms_norm_kernel<DT, NCH, true>), dim3(grid), dim3(256), 0, s, a);
+  if (a.part) {
+    hipLaunchKernelGGL((add_rms_norm_kernel<DT, NCH, true, true>), dim3(grid), dim3(256), 0, s, a);
+  } else if (a.r) {
+    hipLaunchKernelGGL((add_rms_norm_kernel<DT, NCH, true, false>), dim3(grid), dim3(256), 0, s, a);
   } else {
-    hipLaunchKernelGGL((add_rms_norm_kernel<DT, NCH, false>), dim3(grid), dim3(256), 0, s, a);
+    hipLaunchKernelGGL((add_rms_norm_kernel<DT, NCH, false, false>), dim3(grid), dim3(256), 0, s, a);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -283,7 +348,47 @@ extern "C" int nimbus_add_rms_norm(const void* x, int64_t x_stride, const void* 
   a.rows = static_cast<int32_t>(rows);
   a.cols = cols;
   a.eps = eps;
+  a.part = nullptr;
+  a.plane = 0;
+  a.splits = 0;
+  a.pscale = nullptr;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!chunked) return dtype == kFloat16 ? launch_norm_general<kFloat16>(a, s) : launch_norm_general<kBFloat16>(a, s);
+  return dtype == kFloat16 ? launch_norm<kFloat16>(a, s) : launch_norm<kBFloat16>(a, s);
+}
+
+extern "C" int nimbus_add_rms_norm_partials(const float* partials, int32_t splits, const void* scale,
+                                            const void* residual, int64_t residual_stride, const void* weight,
+                                            void* out, int64_t out_stride, void* residual_out,
+                                            int64_t residual_out_stride, int64_t rows, int32_t cols, float eps,
+                                            int32_t dtype, void* stream) {
+  if (rows < 0 || cols <= 0 || splits < 1) return NIMBUS_ERR_INVALID;
+  if (dtype != kFloat16 && dtype != kBFloat16) return NIMBUS_ERR_UNSUPPORTED;
+  if (rows > INT32_MAX || cols % 8 != 0 || cols > 256 * kNormMaxChunksPerLane * 8) return NIMBUS_ERR_UNSUPPORTED;
+  if (rows == 0) return NIMBUS_OK;
+  if (!partials || !scale || !residual || !weight || !out || !residual_out) return NIMBUS_ERR_INVALID;
+  if (residual_stride < cols || out_stride < cols || residual_out_stride < cols) return NIMBUS_ERR_INVALID;
+  const uintptr_t ptrs = reinterpret_cast<uintptr_t>(partials) | reinterpret_cast<uintptr_t>(scale) |
+                         reinterpret_cast<uintptr_t>(residual) | reinterpret_cast<uintptr_t>(weight) |
+                         reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual_out);
+  if (ptrs % 16 != 0 || (residual_stride | out_stride | residual_out_stride) % 8 != 0) return NIMBUS_ERR_ALIGNMENT;
+  NormArgs a;
+  a.x = nullptr;
+  a.sx = 0;
+  a.r = static_cast<const uint16_t*>(residual);
+  a.sr = residual_stride;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.out = static_cast<uint16_t*>(out);
+  a.so = out_stride;
+  a.rout = static_cast<uint16_t*>(residual_out);
+  a.sro = residual_out_stride;
+  a.rows = static_cast<int32_t>(rows);
+  a.cols = cols;
+  a.eps = eps;
+  a.part = partials;
+  a.plane = rows * cols;
+  a.splits = splits;
+  a.pscale = static_cast<const uint16_t*>(scale);
+  hipStream_t s = static_cast<hipStream_t>(stream);
   return dtype == kFloat16 ? launch_norm<kFloat16>(a, s) : launch_norm<kBFloat16>(a, s);
 }

@@ -14,6 +14,8 @@ wave then streams its weights contiguously instead of 64 bytes per row.
 
 from __future__ import annotations
 
+from dataclasses import dataclass
+
 import torch
 
 from nimbus_amd import _lib
@@ -326,3 +328,53 @@ def int8_matmul_packed_silu(x: torch.Tensor, w_packed: torch.Tensor, scale: torc
                                             _lib.stream_of(x))
     _lib.check(rc, "nimbus_int8_matmul_packed_silu")
     return y.view(*shape[:-1], h) if out is None else y
+
+
+# Set False to have int8_matmul_packed_deferred always reduce (for comparisons).
+DEFER_SPLITS = True
+
+
+@dataclass
+class SplitPartials:
+    """An INT8 projection's output left in its split-K partials: partials
+    [splits, m, n] fp32 (a view of the per-stream INT8 workspace, valid until
+    the next INT8 call on the stream), the channel scale, and the output's
+    shape and dtype. add_rms_norm_partials folds it in, bit for bit as the
+    reducing launch would have formed the output."""
+
+    partials: torch.Tensor
+    scale: torch.Tensor
+    shape: tuple
+    dtype: torch.dtype
+
+
+def int8_matmul_packed_deferred(x: torch.Tensor, w_packed: torch.Tensor, scale: torch.Tensor, n: int,
+                                k: int) -> torch.Tensor | SplitPartials:
+    """int8_matmul_packed(x, w_packed, scale, n, k), except that where its
+    tuned plan splits K the output is returned as its unreduced partials
+    (SplitPartials) for the residual add + RMSNorm that reads it next, which
+    saves the reducing launch. n a multiple of 8 and at most 8192 (the rows
+    that norm takes); otherwise, or when the plan does not split, a tensor."""
+    m = x.numel() // max(x.shape[-1], 1) if x.dim() else 0
+    if (not DEFER_SPLITS or n % 8 != 0 or n > 8192 or m == 0 or x.dim() < 1 or x.shape[-1] != k
+            or x.dtype not in (torch.float16, torch.bfloat16)):
+        return int8_matmul_packed(x, w_packed, scale, n, k)
+    x2 = x.reshape(-1, k)
+    key = (m_bucket(m), n, k, x.dtype, x.device.index)
+    if key not in _TUNED:
+        return int8_matmul_packed(x, w_packed, scale, n, k)  # (tunes: the next call takes the tuned plan)
+    plan = _TUNED[key]
+    lib = _lib.load()
+    need = lib.nimbus_int8_matmul_packed_plan_workspace_bytes(m, n, k, *plan) if plan is not None else 0
+    if need <= 0:
+        return int8_matmul_packed(x, w_packed, scale, n, k)
+    if x2.stride(-1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    ws = _cached_workspace(need, x.device, _INT8_WORKSPACES)
+    rc = lib.nimbus_int8_matmul_packed_partials(x2.data_ptr(), x2.stride(0), w_packed.data_ptr(), m, n, k, *plan,
+                                                ws.data_ptr(), ws.numel() * ws.element_size(),
+                                                _lib.dtype_code(x.dtype), _lib.stream_of(x))
+    _lib.check(rc, "nimbus_int8_matmul_packed_partials")
+    splits = need // (m * n * 4)
+    part = ws.view(torch.uint8)[:need].view(torch.float32).view(splits, m, n)
+    return SplitPartials(part, scale.contiguous(), tuple(x.shape[:-1]) + (n,), x.dtype)

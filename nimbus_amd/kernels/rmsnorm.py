@@ -69,3 +69,26 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
 def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
     """residual += x; returns (rms_norm(residual), residual). Does not modify inputs."""
     return _launch(x, residual, weight, eps)
+
+
+def add_rms_norm_partials(p, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """add_rms_norm(h, residual, weight, eps) where h is the INT8 projection
+    output that p (kernels.int8_matmul.SplitPartials) stands for: one launch
+    folds its split-K partials in as the reducing launch would, then adds and
+    normalises; the same bits as the two launches. Returns (out, residual)."""
+    splits, m, n = p.partials.shape
+    if residual.shape != p.shape or residual.dtype != p.dtype or weight.shape != (n,) or weight.dtype != p.dtype:
+        raise ValueError(f"residual {tuple(residual.shape)} / weight {tuple(weight.shape)} do not match {p.shape}")
+    if weight.stride(0) != 1:
+        weight = weight.contiguous()
+    r2 = residual.reshape(m, n)
+    if r2.stride(-1) != 1:
+        r2 = r2.contiguous()
+    out = torch.empty((m, n), dtype=p.dtype, device=residual.device)
+    rout = torch.empty_like(out)
+    lib = _lib.load()
+    rc = lib.nimbus_add_rms_norm_partials(p.partials.data_ptr(), splits, p.scale.data_ptr(), r2.data_ptr(),
+                                          r2.stride(0), weight.data_ptr(), out.data_ptr(), n, rout.data_ptr(), n,
+                                          m, n, float(eps), _lib.dtype_code(p.dtype), _lib.stream_of(residual))
+    _lib.check(rc, "nimbus_add_rms_norm_partials")
+    return out.view(p.shape), rout.view(p.shape)

@@ -23,7 +23,8 @@ from torch import nn
 
 from nimbus_amd.kernels import cache_ops
 from nimbus_amd.kernels.elementwise import rope_, silu_mul
-from nimbus_amd.kernels.rmsnorm import add_rms_norm, rms_norm
+from nimbus_amd.kernels.int8_matmul import SplitPartials
+from nimbus_amd.kernels.rmsnorm import add_rms_norm, add_rms_norm_partials, rms_norm
 from nimbus_amd.model.attention import AttentionBackend, AttnMetadata
 from nimbus_amd.model.config import ModelConfig
 
@@ -86,9 +87,11 @@ class RMSNorm(nn.Module):
         self.eps = eps
         del fused
 
-    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None):
+    def forward(self, x, residual: torch.Tensor | None = None):
         if residual is None:
             return rms_norm(x, self.weight, self.eps)
+        if isinstance(x, SplitPartials):  # an INT8 projection's output, still in its split-K partials
+            return add_rms_norm_partials(x, residual, self.weight, self.eps)
         return add_rms_norm(x, residual, self.weight, self.eps)
 
 
@@ -101,12 +104,13 @@ class Attention(nn.Module):
         self.scale = self.d ** -0.5
         self.backend = backend
 
-    def forward(self, x, positions, rotary: Rotary, k_cache, v_cache, meta: AttnMetadata):
+    def forward(self, x, positions, rotary: Rotary, k_cache, v_cache, meta: AttnMetadata, deferred: bool = False):
         """nimbus/model/llama.py:88-98. One launch rotates the q and k heads
         of each qkv row in place and writes the k and v heads into the cache
         (the backend's first step, nimbus/model/attention.py:78), so the
         backend is told the cache already holds them; q goes to it as a
-        strided view (no copy)."""
+        strided view (no copy). deferred: an INT8 o_proj may return its
+        split-K partials for the next norm to fold in."""
         t = x.shape[0]
         hd, kvd = self.h * self.d, self.kv * self.d
         qkv = self.qkv_proj(x)
@@ -116,7 +120,8 @@ class Attention(nn.Module):
         k = qkv[:, hd:hd + kvd].view(t, self.kv, self.d)
         v = qkv[:, hd + kvd:].view(t, self.kv, self.d)
         o = self.backend.forward(q, k, v, k_cache, v_cache, meta, self.scale, kv_written=True)
-        return self.o_proj(o.view(t, hd))
+        proj = getattr(self.o_proj, "forward_deferred", None) if deferred else None
+        return proj(o.view(t, hd)) if proj is not None else self.o_proj(o.view(t, hd))
 
 
 class MLP(nn.Module):
@@ -126,7 +131,7 @@ class MLP(nn.Module):
         self.gate_up_proj = nn.Linear(cfg.hidden_size, 2 * self.inter, bias=False)
         self.down_proj = nn.Linear(self.inter, cfg.hidden_size, bias=False)
 
-    def forward(self, x):
+    def forward(self, x, deferred: bool = False):
         # An INT8 gate_up projection runs with the SiLU gate in its epilogue
         # (one launch and no [M, 2I] output; the two steps' bits under the
         # same launch plan).
@@ -134,7 +139,10 @@ class MLP(nn.Module):
         h = fused(x) if fused is not None else None
         if h is None:
             h = silu_mul(self.gate_up_proj(x))
-        return self.down_proj(h)
+        # deferred: an INT8 down_proj may return its split-K partials for the
+        # next norm to fold in
+        proj = getattr(self.down_proj, "forward_deferred", None) if deferred else None
+        return proj(h) if proj is not None else self.down_proj(h)
 
 
 class DecoderLayer(nn.Module):
@@ -153,9 +161,11 @@ class DecoderLayer(nn.Module):
             h = self.input_layernorm(x)
         else:
             h, residual = self.input_layernorm(x, residual)
-        h = self.self_attn(h, positions, rotary, k_cache, v_cache, meta)
+        # (the projections into the two norms may hand over an INT8 output
+        # still in split-K partials; the norm folds them in)
+        h = self.self_attn(h, positions, rotary, k_cache, v_cache, meta, deferred=True)
         h, residual = self.post_attention_layernorm(h, residual)
-        return self.mlp(h), residual
+        return self.mlp(h, deferred=True), residual
 
 
 class LlamaModel(nn.Module):

@@ -13,8 +13,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from nimbus_amd.kernels.int8_matmul import (int8_matmul_packed, int8_matmul_packed_silu, pack_int8_weight,
-                                             unpack_int8_weight)
+from nimbus_amd.kernels.int8_matmul import (int8_matmul_packed, int8_matmul_packed_deferred, int8_matmul_packed_silu,
+                                             pack_int8_weight, unpack_int8_weight)
 
 
 def quantize_weight(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -57,6 +57,12 @@ class Int8Linear(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return int8_matmul_packed(x, self.weight_packed, self.scale, self.out_features, self.in_features)
+
+    def forward_deferred(self, x: torch.Tensor):
+        """self(x), or where the tuned launch plan splits K its unreduced
+        partials (kernels.int8_matmul.SplitPartials), for the decoder layer's
+        residual add + RMSNorm to fold in (the same bits, one launch fewer)."""
+        return int8_matmul_packed_deferred(x, self.weight_packed, self.scale, self.out_features, self.in_features)
 
     def forward_silu(self, x: torch.Tensor) -> torch.Tensor | None:
         """silu_mul(self(x)) in one launch, for the MLP's gate_up projection

@@ -222,6 +222,37 @@ def test_int8_matmul_rejects_before_launch():
     assert ws(-1, 4, 16) == -1
 
 
+def test_split_partials_entries_reject_before_launch():
+    """The split-K partials of a projection and the norm that folds them in
+    refuse plans that do not split, short workspaces, rows the norm's chunked
+    kernel does not take, missing pointers and misalignment, before any
+    launch."""
+    lib = _lib.load()
+    part = lib.nimbus_int8_matmul_packed_partials
+    pargs = lambda **kw: dict(x=DUMMY, xs=4096, w=DUMMY, m=64, n=4096, k=4096, bm=64, ks=1, splits=4, rw=1,
+                              ws=DUMMY, wsb=1 << 30, dt=1, stream=None) | kw
+    call = lambda f, d: f(*d.values())
+    assert call(part, pargs(m=-1)) == _lib.NIMBUS_ERR_INVALID
+    assert call(part, pargs(splits=1)) == _lib.NIMBUS_ERR_UNSUPPORTED  # no split: nothing to leave unreduced
+    assert call(part, pargs(bm=48)) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert call(part, pargs(dt=5)) == _lib.NIMBUS_ERR_UNSUPPORTED
+    assert call(part, pargs(m=0)) == 0
+    assert call(part, pargs(x=None)) == _lib.NIMBUS_ERR_INVALID
+    assert call(part, pargs(ws=None)) == _lib.NIMBUS_ERR_WORKSPACE
+    assert call(part, pargs(wsb=4 * 64 * 4096 * 4 - 4)) == _lib.NIMBUS_ERR_WORKSPACE
+    assert call(part, pargs(x=DUMMY + 8)) == _lib.NIMBUS_ERR_ALIGNMENT
+    norm = lib.nimbus_add_rms_norm_partials
+    nargs = lambda **kw: dict(p=DUMMY, splits=4, s=DUMMY, r=DUMMY, rs=4096, w=DUMMY, o=DUMMY, os=4096, ro=DUMMY,
+                              ros=4096, rows=64, cols=4096, eps=1e-5, dt=1, stream=None) | kw
+    assert call(norm, nargs(splits=0)) == _lib.NIMBUS_ERR_INVALID
+    assert call(norm, nargs(cols=4100)) == _lib.NIMBUS_ERR_UNSUPPORTED  # not a multiple of 8
+    assert call(norm, nargs(cols=16384, rs=16384, os=16384, ros=16384)) == _lib.NIMBUS_ERR_UNSUPPORTED  # past 8192
+    assert call(norm, nargs(rows=0)) == 0
+    assert call(norm, nargs(r=None)) == _lib.NIMBUS_ERR_INVALID  # the residual is required
+    assert call(norm, nargs(rs=4000)) == _lib.NIMBUS_ERR_INVALID
+    assert call(norm, nargs(s=DUMMY + 8)) == _lib.NIMBUS_ERR_ALIGNMENT
+
+
 def test_int8_packed_silu_rejects_before_launch():
     """The fused gate_up + SiLU entry refuses shapes, plans, null pointers,
     short strides and misalignment with an error code, before any launch."""

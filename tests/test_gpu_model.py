@@ -315,6 +315,49 @@ def test_int8_decode_graphs_match_eager(n, dtype):
                 s.feed(t)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_int8_split_partials_folded_into_the_norms_give_the_same_logits(dtype):
+    """With split plans for o_proj and down_proj (forced here; the tuner
+    picks them where they are faster), the decoder layer's norms fold the
+    projections' split-K partials in themselves: the logits are bit for bit
+    those of the same model with the partials reduced by their own launch,
+    over a prefill step and decode steps, eager and graph-replayed."""
+    from nimbus_amd.kernels import int8_matmul as im
+
+    announce(f"int8 split partials into the norms {dtype}")
+    model, caches, seqs = _setup(dtype, [9, 30, 4, 51, 17], num_blocks=160, seed=13)
+    quantize_model(model)
+    saved = dict(im._TUNED)
+    try:
+        for m in (1, 2, 4, 8, 16, 32, 64, 111):  # every bucket the steps below use
+            for n, k in ((CFG.hidden_size, CFG.num_heads * CFG.head_dim), (CFG.hidden_size, CFG.intermediate_size)):
+                im._TUNED[(im.m_bucket(m), n, k, dtype, 0)] = (16, 1, 2, 1)
+        runs = []
+        for defer in (True, False):
+            im.DEFER_SPLITS = defer
+            c, ss = _clone_caches(caches), _clone_seqs(seqs)
+            _, lg = _eager_step(model, c, [(s, len(s)) for s in ss])
+            out = [lg]
+            for s, t in zip(ss, lg.argmax(-1).tolist()):
+                s.feed(t)
+            graphs = DecodeGraphs(model, c, BS, max_model_len=512, max_batch=8, scratch_block=160,
+                                  num_kv_heads=CFG.num_kv_heads, device="cuda")
+            graphs.capture()
+            for _ in range(3):
+                lg = graphs.run(ss).clone()
+                out.append(lg)
+                for s, t in zip(ss, lg.argmax(-1).tolist()):
+                    s.feed(t)
+            torch.cuda.synchronize()
+            runs.append(out)
+        for a, b in zip(*runs):
+            assert torch.equal(a, b)
+    finally:
+        im.DEFER_SPLITS = True
+        im._TUNED.clear()
+        im._TUNED.update(saved)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("heads,d", [(40, 128), (6, 64)])
 def test_rope_kernel_is_the_reference_arithmetic(dtype, heads, d):

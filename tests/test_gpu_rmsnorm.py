@@ -179,3 +179,42 @@ def test_residual_out_may_alias_an_input(dtype, cols, alias):
     torch.cuda.synchronize()
     assert torch.equal(_bits(dst.cpu()), _bits(want_r))
     assert_norm_close(out.cpu(), want_y)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("m,n,k,plan", [(64, 4096, 14336, (64, 2, 4, 1)), (64, 4096, 4096, (64, 1, 8, 1)),
+                                        (7, 2048, 5632, (16, 1, 3, 2)), (300, 1024, 2048, (64, 1, 2, 1))])
+def test_norm_folding_split_partials_equals_reduce_then_norm(dtype, m, n, k, plan):
+    """An INT8 projection left in split-K partials and the residual add +
+    RMSNorm that folds them in give, bit for bit, the projection's reduced
+    output followed by nimbus_add_rms_norm (the same plan), both outputs."""
+    from nimbus_amd import _lib
+    from nimbus_amd.kernels.int8_matmul import SplitPartials, pack_int8_weight
+    from nimbus_amd.kernels.rmsnorm import add_rms_norm_partials
+    from nimbus_amd.quant import quantize_weight
+
+    announce(f"add_rms_norm of split partials m={m} n={n} k={k} plan={plan} {dtype}")
+    lib = _lib.load()
+    g = torch.Generator(device="cuda").manual_seed(m + n + k)
+    wq, sc = quantize_weight((torch.randn(n, k, generator=g, device="cuda") * 0.02).to(dtype))
+    wp = pack_int8_weight(wq)
+    x = torch.randn(m, k, generator=g, device="cuda").to(dtype)
+    r = torch.randn(m, n, generator=g, device="cuda").to(dtype)
+    w = torch.randn(n, generator=g, device="cuda").to(dtype)
+    need = lib.nimbus_int8_matmul_packed_plan_workspace_bytes(m, n, k, *plan)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    st, dt = _lib.stream_of(x), _lib.dtype_code(dtype)
+    y = torch.empty(m, n, dtype=dtype, device="cuda")
+    _lib.check(lib.nimbus_int8_matmul_packed_plan(x.data_ptr(), k, wp.data_ptr(), sc.data_ptr(), y.data_ptr(), n,
+                                                  m, n, k, *plan, ws.data_ptr(), need, dt, st), "plan")
+    want_y, want_r = add_rms_norm(y, r, w, 1e-5)
+    ws2 = torch.full((need,), 255, dtype=torch.uint8, device="cuda")  # stale bytes: every partial is written
+    _lib.check(lib.nimbus_int8_matmul_packed_partials(x.data_ptr(), k, wp.data_ptr(), m, n, k, *plan,
+                                                      ws2.data_ptr(), need, dt, st), "partials")
+    splits = need // (m * n * 4)
+    p = SplitPartials(ws2.view(torch.float32).view(splits, m, n), sc, (m, n), dtype)
+    got_y, got_r = add_rms_norm_partials(p, r, w, 1e-5)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(got_r), _bits(want_r))
+    assert torch.equal(_bits(got_y), _bits(want_y))
